@@ -1,0 +1,237 @@
+"""Quest decode layer-step benchmark on one MI355X.
+
+Workload (default): batch 16, every request at 128K context (131072 tokens),
+Qwen3-30B-A3B attention shape (32 q heads, 4 KV heads, head_dim 128, bf16),
+Quest page 64, top_k 2048 (31 pages + recent 64), quest mode: all 48 layers'
+K/V pools (about 192 GiB) and page bounds (3 GiB) resident in HBM, inputs
+synthetic N(0, 1) from fixed seeds.
+
+One step = one decode step of all 48 layers through the drop-in backend:
+bounds append (fused over layers) + per layer: new K/V write, GQA-mean page
+scoring + top-31 selection + layout, req_to_token gather + split-K attention.
+The step is captured once in a HIP graph and replayed; seq_lens advance by one
+token per replay, so pages complete and get finalized during the run.
+Reported value: microseconds per layer-step (step time / 48).
+
+    python bench.py [--steps K] [--warmup W]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+
+
+class Layer:
+    def __init__(self, layer_id: int, scaling: float):
+        self.layer_id, self.scaling = layer_id, scaling
+
+
+def algorithmic_bytes(seqs, page: int, top_k: int, row_bytes: int, page_bytes: int) -> dict:
+    """Per layer-step: bounds of complete pages + K/V of the attended rows (+ small terms)."""
+    bounds = sum((s // page) * page_bytes for s in seqs)
+    kv = sum(min(s, top_k) * row_bytes for s in seqs)
+    return {"bounds": bounds, "kv": kv, "headline": bounds + kv}
+
+
+def time_graph(fn, reps: int, stream) -> float:
+    """Average ms of one call of fn, from a graph holding `reps` calls, timed with HIP events."""
+    fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(reps):
+            fn()
+    g.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(3):
+        g.replay()
+    end.record(stream)
+    end.synchronize()
+    return start.elapsed_time(end) / (3 * reps)
+
+
+def cpu_baseline(top_k, page, heads, kv, dim, ctx, sample_reqs: int) -> dict:
+    """The oracle (numpy, one core) on `sample_reqs` requests of one layer at full context."""
+    from oracle import attention as oa
+    from oracle import bf16
+    from oracle import quest as oq
+
+    rng = np.random.default_rng(7)
+    n_pages = ctx // page
+    times = []
+    for _ in range(sample_reqs):
+        bounds = bf16.from_f32(np.sort(rng.standard_normal((n_pages, kv, dim, 2), dtype=np.float32), axis=-1))
+        k = bf16.round_f32(rng.standard_normal((ctx, kv, dim), dtype=np.float32))
+        v = bf16.round_f32(rng.standard_normal((ctx, kv, dim), dtype=np.float32))
+        q = bf16.round_f32(rng.standard_normal((1, heads, dim), dtype=np.float32))
+        t0 = time.perf_counter()
+        qbar = oq.group_queries(q, kv, dim, is_bf16=True)
+        lay = oq.step_layout([ctx], page, top_k, False)
+        pos, actual, _ = oq.retrieve_topk(qbar, bounds[None], lay, page, top_k)
+        oa.sparse_decode(q, k, v, [pos[0, : int(actual[0])]], dim**-0.5)
+        times.append(time.perf_counter() - t0)
+    return {"per_request_s": float(np.median(times)), "reqs": sample_reqs}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--batch", type=int, default=16)
+    ap.add_argument("--ctx", type=int, default=131072)
+    ap.add_argument("--layers", type=int, default=48)
+    ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--cpu-sample", type=int, default=2, help="requests in the CPU-baseline sample (0 = skip)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: the path shards by request with no cross-GPU traffic, "
+              "and this build runs on a single MI355X; use --gpus 1", file=sys.stderr)
+        return 2
+
+    from qwenquest_amd import _lib
+    from qwenquest_amd.attention.quest_only import QuestOnlyBackend
+    from qwenquest_amd.batch import ForwardBatch, ForwardMode
+    from qwenquest_amd.memory import MHATokenToKVPool, ReqToTokenPool
+
+    _lib.load()
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    B, S, L = args.batch, args.ctx, args.layers
+    H, KV, D, P, TOP_K = 32, 4, 128, 64, 2048
+    total_steps = args.warmup + args.steps + 2
+    max_ctx = S + total_steps + 64
+    rows = B * max_ctx
+
+    t_setup = time.perf_counter()
+    rtp = ReqToTokenPool(B, max_ctx, dev)
+    kvp = MHATokenToKVPool(rows, L, KV, D, torch.bfloat16, dev)
+    gen = torch.Generator(device=dev).manual_seed(1234)
+    for layer in range(L):
+        kvp.k_all[layer].normal_(generator=gen)
+        kvp.v_all[layer].normal_(generator=gen)
+    base = 1 + torch.arange(B, device=dev, dtype=torch.int64) * max_ctx
+    rtp.req_to_token.copy_((base[:, None] + torch.arange(max_ctx, device=dev)[None]).to(torch.int32))
+    be = QuestOnlyBackend(rtp, kvp, {"algorithm": "quest", "top_k": TOP_K, "quest_page_size": P})
+    prompt = S - 1  # prefill covers positions [0, S-1); the first decode step has seq_len S
+    for r in range(B):
+        be.quest.update_prefill_representations_fused(r, kvp.k_all, rtp.req_to_token[r, :prompt])
+        be._skip_first_decode_update[r] = True
+    q_all = torch.randn((L, B, H, D), generator=gen, device=dev).to(torch.bfloat16)
+    k_new = torch.randn((L, B, KV, D), generator=gen, device=dev).to(torch.bfloat16)
+    v_new = torch.randn((L, B, KV, D), generator=gen, device=dev).to(torch.bfloat16)
+    layers = [Layer(i, D**-0.5) for i in range(L)]
+    rpi = torch.arange(B, device=dev, dtype=torch.int64)
+    seq_lens = torch.full((B,), S, device=dev, dtype=torch.int64)
+    out_loc = torch.empty(B, device=dev, dtype=torch.int64)
+    torch.cuda.synchronize()
+    setup_s = time.perf_counter() - t_setup
+
+    batch = ForwardBatch(ForwardMode.DECODE, None, None, rpi, seq_lens, out_loc, rtp, kvp, be)
+
+    def step():
+        torch.add(base, seq_lens - 1, out=out_loc)
+        be.init_forward_metadata(batch)
+        for layer in range(L):
+            be.forward_decode(q_all[layer], k_new[layer], v_new[layer], layers[layer], batch)
+        seq_lens.add_(1)
+
+    stream = torch.cuda.current_stream()
+    step()  # eager: first decode step after prefill (bounds fold skipped), allocates workspaces
+    torch.cuda.synchronize()
+    if args.no_graph:
+        run = step
+    else:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step()
+        run = graph.replay
+    for _ in range(args.warmup):
+        run()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        run()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_per_step = elapsed * 1e3 / args.steps
+    us_per_layer_step = ms_per_step * 1e3 / L
+
+    seqs_timed = [S + 1 + args.warmup + args.steps // 2] * B
+    byts = algorithmic_bytes(seqs_timed, P, TOP_K, 2 * KV * D * 2, KV * D * 2 * 2)
+    step_frac = byts["headline"] / (us_per_layer_step * 1e-6) / (HBM_PEAK_GBS * 1e9)
+
+    # per-kernel durations: graph of 48 launches of one family at the same shapes
+    quest = be.quest
+    pos_buf = be._positions
+    quest.prepare_step(seq_lens)
+
+    def score_select():
+        quest.retrieve_topk(q_all[0], 0, rpi, seq_lens, out=pos_buf)
+
+    def attend():
+        be.sparse_attention(q_all[0], layers[0], rpi, pos_buf[:B], quest._step.actual_lens, B)
+
+    ms_sel = time_graph(score_select, L, stream)
+    ms_att = time_graph(attend, L, stream)
+    bw_sel = byts["bounds"] / (ms_sel * 1e-3) / 1e9
+    bw_att = byts["kv"] / (ms_att * 1e-3) / 1e9
+    dominant = ("quest_decode_attention", ms_att, byts["kv"], bw_att) if ms_att >= ms_sel else (
+        "quest_score_select", ms_sel, byts["bounds"], bw_sel)
+
+    cpu = None
+    if args.cpu_sample > 0:
+        cores = 1
+        c = cpu_baseline(TOP_K, P, H, KV, D, S, args.cpu_sample)
+        us_cpu = c["per_request_s"] * B * 1e6
+        cpu = {"value": round(us_cpu, 1), "unit": "us per layer-step", "cores": cores, "kind": "port",
+               "sample": f"numpy oracle, {args.cpu_sample} requests x 1 layer at {S} tokens "
+                         f"(score+select+gather+attention), median per request x {B}"}
+
+    line = {
+        "metric": "µs per Quest decode layer-step @128K ctx, batch 16; % peak HBM BW",
+        "value": round(us_per_layer_step, 2),
+        "unit": "us per layer-step",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic N(0,1) q/k/v, fixed seeds",
+        "config": {"workload": f"quest decode, batch {B}, {S}-token context, {L} layers, "
+                               f"32q/4kv heads x 128, page 64, top_k 2048",
+                   "batch": B, "seq_len": S, "layers": L, "graph": not args.no_graph},
+        "hbm_frac_layer_step": round(step_frac, 4),
+        "tokens_per_s": round(B / (ms_per_step * 1e-3), 1),
+        "algorithmic_bytes_per_layer_step": byts,
+        "kernels_us": {"quest_score_select": round(ms_sel * 1e3, 2),
+                       "quest_decode_attention": round(ms_att * 1e3, 2)},
+        "roofline": {"kernel": dominant[0], "bound": "hbm", "achieved": round(dominant[3], 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(dominant[3] / HBM_PEAK_GBS, 4),
+                     "traffic": None},
+        "cpu_baseline": cpu,
+        "setup_s": round(setup_s, 1),
+    }
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

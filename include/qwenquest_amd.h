@@ -1,0 +1,182 @@
+/*
+ * qwenquest_amd - C ABI of the MI355X (gfx950) Quest sparse-decode library.
+ *
+ * Every entry point enqueues HIP kernels on `stream` (a hipStream_t passed as
+ * void*; NULL = the default stream) and returns a status:
+ *   QQ_OK (0), QQ_EINVAL (bad argument; the Python side raises ValueError),
+ *   QQ_ERUNTIME (ordering / capacity; RuntimeError), QQ_EHIP (a HIP error).
+ * qq_last_error() returns the message of the last failure on this thread.
+ *
+ * The library never allocates: the caller owns every buffer (device memory
+ * for tensors and workspaces, pinned host memory for the HiSparse host tier)
+ * and passes raw pointers plus explicit geometry.  All tensors are dense,
+ * row-major, in the layouts of the reference (wengyinqi/QwenQuest):
+ *   page_k_bounds  [L, R, MP, KV, D, 2] bf16  (min, max) interleaved
+ *   running_k_min/max [L, R, KV, D] bf16, running counters [R] int32
+ *   req_to_token   [R, max_ctx] int32,  K/V pool of a layer [rows, KV, D]
+ * bf16 tensors are passed as uint16_t bit patterns.
+ *
+ * Reference file:line citations are relative to the reference repository root.
+ */
+#ifndef QWENQUEST_AMD_H
+#define QWENQUEST_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QQ_OK 0
+#define QQ_EINVAL (-1)
+#define QQ_ERUNTIME (-2)
+#define QQ_EHIP (-3)
+
+#define QQ_DTYPE_BF16 0
+#define QQ_DTYPE_F32 1
+
+/* Library version (major*10000 + minor*100 + patch). */
+int qq_version(void);
+/* Message of the last failing call on this thread ("" if none). */
+const char* qq_last_error(void);
+
+/* ------------------------------------------------------------ Quest storage
+ * Replaces QuestAlgorithm.init_storage's sentinel fill (src/qwenquest/quest.py:194-208)
+ * and QuestAlgorithm.invalidate_request (src/qwenquest/quest.py:468-479):
+ * resets requests [req_begin, req_begin + req_count) in every layer - page
+ * bounds to (min=+bf16max, max=-bf16max), running bounds to the same
+ * sentinels, both counters to 0. */
+int qq_quest_reset(uint16_t* page_k_bounds, uint16_t* running_k_min, uint16_t* running_k_max,
+                   int32_t* running_token_count, int32_t* running_page_idx, int num_layers,
+                   int max_reqs, int max_pages, int kv_heads, int head_dim, int req_begin,
+                   int req_count, void* stream);
+
+/* Replaces QuestAlgorithm.update_prefill_representations
+ * (src/qwenquest/quest.py:231-280), fused over `n_layers` consecutive layers
+ * starting at layer offset `layer_begin` (upstream's
+ * update_prefill_representations_fused).  Keys of layer (layer_begin + i) are
+ * read from `k_base + i * k_layer_stride` (elements, `k_rows` rows of KV*D
+ * elements; rows outside [0, k_rows) are skipped), gathered through
+ * `prefill_indices` (int32 or int64, `n_tokens` entries in position order).
+ * Complete pages go to page_k_bounds, the partial tail to the running bounds;
+ * when `set_counters` the request's counters become (n % P, n / P)
+ * (the reference does this on the last layer, quest.py:278-280). */
+int qq_quest_prefill_bounds(const void* k_base, int64_t k_layer_stride, int k_dtype,
+                            int64_t k_rows, const void* prefill_indices, int indices_are_int64, int64_t n_tokens,
+                            int req, int layer_begin, int n_layers, int set_counters,
+                            uint16_t* page_k_bounds, uint16_t* running_k_min,
+                            uint16_t* running_k_max, int32_t* running_token_count,
+                            int32_t* running_page_idx, int num_layers, int max_reqs, int max_pages,
+                            int kv_heads, int head_dim, int page_size, void* stream);
+
+/* Replaces QuestAlgorithm.update_decode_representations
+ * (src/qwenquest/quest.py:284-302) for layers [layer_begin, layer_begin + n_layers):
+ * folds the key at row `device_locs[i]` into request `req_indices[i]`'s
+ * running min/max.  An entry with device_locs[i] < 0 is skipped entirely (the
+ * reference drops such requests from the call: quest_only.py:88-92).  With `finalize` != 0 (requires the full layer range) it
+ * also performs maybe_finalize_decode_representations (quest.py:304-321) in
+ * the same pass - upstream's update_decode_representations_fused. */
+int qq_quest_decode_update(const void* k_base, int64_t k_layer_stride, int k_dtype,
+                           int64_t k_rows, const int64_t* req_indices, const int64_t* device_locs, int n,
+                           int layer_begin, int n_layers, int finalize, uint16_t* page_k_bounds,
+                           uint16_t* running_k_min, uint16_t* running_k_max,
+                           int32_t* running_token_count, int32_t* running_page_idx,
+                           int num_layers, int max_reqs, int max_pages, int kv_heads,
+                           int head_dim, int page_size, void* stream);
+
+/* Replaces QuestAlgorithm.maybe_finalize_decode_representations
+ * (src/qwenquest/quest.py:304-321): for requests whose running_token_count is
+ * P-1, copy the running bounds into page running_page_idx (all layers), reset
+ * them, advance the page index; every listed request's count becomes (c+1)%P. */
+int qq_quest_decode_finalize(const int64_t* req_indices, int n, uint16_t* page_k_bounds,
+                             uint16_t* running_k_min, uint16_t* running_k_max,
+                             int32_t* running_token_count, int32_t* running_page_idx,
+                             int num_layers, int max_reqs, int max_pages, int kv_heads,
+                             int head_dim, int page_size, void* stream);
+
+/* Replaces QuestAlgorithm.prepare_step (src/qwenquest/quest.py:325-362):
+ * actual_lens = min(seq, top_k); candidate_limit = seq / P, or max(seq/P - 1, 0)
+ * with avoid_recent_overlap.  The recent window and the dense layout are
+ * produced directly by qq_quest_retrieve_topk. */
+int qq_quest_prepare_step(const int64_t* seq_lens, int bs, int page_size, int top_k,
+                          int avoid_recent_overlap, int32_t* actual_lens,
+                          int32_t* candidate_limit, void* stream);
+
+/* Replaces QuestAlgorithm.retrieve_topk (src/qwenquest/quest.py:409-464)
+ * including group_queries (:366-391) and page_scores (:393-405), for layer
+ * offset `layer`.  q: [bs, num_q_heads, D] (bf16 or fp32) with batch stride
+ * `q_batch_stride` elements.  Writes positions [bs, top_k] int32 (long
+ * requests: the top_k/P - 1 best complete pages by descending score, ties to
+ * the lowest page index, expanded x P, then the recent window; short
+ * requests: 0..seq-1 padded with seq-1).  Page scores of candidate pages are
+ * left in scores_ws [bs, max_pages] fp32.  `tickets` [bs] int32 must be zero
+ * on entry and is zero again on exit. */
+int qq_quest_retrieve_topk(const void* q, int q_dtype, int64_t q_batch_stride, int num_q_heads,
+                           const uint16_t* page_k_bounds, int layer, const int64_t* req_pool_indices,
+                           const int64_t* seq_lens, const int32_t* candidate_limit, int bs,
+                           int max_reqs, int max_pages, int kv_heads, int head_dim, int page_size,
+                           int top_k, float* scores_ws, int32_t* tickets, int32_t* positions,
+                           void* stream);
+
+/* Replaces QuestAlgorithm.group_queries (src/qwenquest/quest.py:366-391):
+ * out[b, h, d] = mean over the G = num_q_heads / kv_heads query heads of KV
+ * head h (fp32 sum in head order, / G, one rounding to q's dtype). */
+int qq_quest_group_queries(const void* q, int q_dtype, int64_t q_batch_stride, int num_q_heads,
+                           int kv_heads, int head_dim, int bs, void* out, void* stream);
+
+/* Replaces QuestAlgorithm.page_scores (src/qwenquest/quest.py:393-405):
+ * scores[b, p] = sum_{h,d} (qbar >= 0 ? qbar*kmax : qbar*kmin) over every page
+ * slot p < max_pages of request req_pool_indices[b] at layer offset `layer`,
+ * fp32 products summed in the canonical order (64 lanes of ceil(KV*D/64)
+ * channels, then a halving tree). */
+int qq_quest_page_scores(const void* grouped_q, int q_dtype, int64_t q_batch_stride,
+                         const uint16_t* page_k_bounds, int layer, const int64_t* req_pool_indices,
+                         int bs, int max_reqs, int max_pages, int kv_heads, int head_dim,
+                         float* scores, void* stream);
+
+/* Workspace bytes qq_*_decode_attention needs for `bs` requests of up to
+ * `max_rows` rows each with `num_q_heads` x `head_dim` outputs. */
+int64_t qq_decode_attention_workspace_bytes(int bs, int max_rows, int num_q_heads, int head_dim);
+
+/* Replaces the Mode-2 gather + attention of QuestOnlyBackend.forward_decode
+ * (src/qwenquest/attention/quest_only.py:149-159) and decode_attention
+ * (src/qwenquest/attention/ops.py:48-66): for request i, attends q[i] over rows
+ * req_to_token[req_pool_indices[i], positions[i, j]] for j < actual_lens[i]
+ * (duplicates counted), softmax(q.k * scale) in fp32, output [bs, H*D] in
+ * q's dtype.  k_layer/v_layer: this layer's [kv_rows, KV, D] pool;
+ * req_to_token: [req_to_token_rows, req_to_token_stride] int32.  Out-of-range
+ * requests, positions or rows read the padding row 0 instead of faulting.
+ * `tickets` [bs] int32 zero on entry and exit. */
+int qq_quest_decode_attention(const void* q, int q_dtype, int64_t q_batch_stride,
+                              int num_q_heads, const void* k_layer, const void* v_layer,
+                              int kv_dtype, int64_t kv_rows, int kv_heads, int head_dim,
+                              const int32_t* req_to_token, int64_t req_to_token_stride,
+                              int64_t req_to_token_rows, const int64_t* req_pool_indices,
+                              const int32_t* positions,
+                              int64_t positions_stride, const int32_t* actual_lens, int bs,
+                              float scale, void* out, void* workspace, int64_t workspace_bytes,
+                              int32_t* tickets, void* stream);
+
+/* Replaces the Mode-3 attention of QuestHiSparseBackend.forward_decode
+ * (src/qwenquest/attention/quest_hisparse.py:294-300): like
+ * qq_quest_decode_attention but rows come directly from `rows` [bs, rows_stride]
+ * int64 (the hot-buffer rows returned by the swap-in). */
+int qq_decode_attention_rows(const void* q, int q_dtype, int64_t q_batch_stride, int num_q_heads,
+                             const void* k_layer, const void* v_layer, int kv_dtype,
+                             int64_t kv_rows, int kv_heads, int head_dim, const int64_t* rows,
+                             int64_t rows_stride, const int32_t* actual_lens, int bs, float scale,
+                             void* out, void* workspace, int64_t workspace_bytes,
+                             int32_t* tickets, void* stream);
+
+/* Replaces MHATokenToKVPool.set_kv_buffer (src/qwenquest/memory.py:114-120):
+ * k_layer[locs[i]] = k[i], v_layer[locs[i]] = v[i] (row = KV*D elements),
+ * converting src_dtype -> buf_dtype. */
+int qq_kv_scatter(void* k_layer, void* v_layer, int buf_dtype, int64_t kv_rows, const void* k,
+                  const void* v, int src_dtype, const int64_t* locs, int n, int64_t row_elems,
+                  void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QWENQUEST_AMD_H */

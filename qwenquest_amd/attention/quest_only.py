@@ -1,0 +1,145 @@
+"""Mode 2 - Quest sparse decode, full KV pool on the GPU
+(reference ``src/qwenquest/attention/quest_only.py``, SGLang ``flashinfer_quest``).
+
+Per decode step::
+
+    init_forward_metadata:  [Q3] fold the previous token's K into the running bounds of
+                                 every layer + finalize completed pages (one fused kernel;
+                                 skipped on the first decode step after prefill)
+                            [Q4] prepare_step
+    forward_decode (x L):   save new K/V -> [Q6] retrieve_topk (score + select + layout)
+                            -> [Q7] req_to_token gather + split-K attention
+"""
+
+from __future__ import annotations
+
+from collections.abc import Mapping
+from typing import TYPE_CHECKING, Any
+
+import torch
+
+from qwenquest_amd import _lib
+from qwenquest_amd.attention.base import AttentionBackend
+from qwenquest_amd.attention.ops import AttentionWorkspace
+from qwenquest_amd.config import SparseConfig, parse_hisparse_config
+from qwenquest_amd.quest import QuestAlgorithm
+
+if TYPE_CHECKING:
+    from qwenquest_amd.batch import ForwardBatch
+    from qwenquest_amd.memory import MHATokenToKVPool, ReqToTokenPool
+
+__all__ = ["QuestOnlyBackend"]
+
+
+class QuestOnlyBackend(AttentionBackend):
+    name = "flashinfer_quest"
+
+    def __init__(
+        self,
+        req_to_token_pool: ReqToTokenPool,
+        token_to_kv_pool: MHATokenToKVPool,
+        sparse_config: str | Mapping[str, Any] | SparseConfig | None,
+        *,
+        start_layer: int = 0,
+        end_layer: int | None = None,
+    ):
+        super().__init__(req_to_token_pool, token_to_kv_pool)
+        cfg = parse_hisparse_config(sparse_config)
+        if cfg.algorithm != "quest" or cfg.quest_page_size is None:
+            raise ValueError("Quest backends require hisparse_config with algorithm='quest'")
+        self.sparse_config = cfg
+        device = token_to_kv_pool.device
+        self.quest = QuestAlgorithm(
+            top_k=cfg.top_k, page_size=cfg.quest_page_size, device=device,
+            avoid_recent_overlap=cfg.avoid_recent_overlap,
+        )
+        self.quest.init_storage(
+            start_layer=start_layer,
+            end_layer=token_to_kv_pool.num_layers if end_layer is None else end_layer,
+            max_reqs=req_to_token_pool.size,
+            max_context_len=req_to_token_pool.max_context_len,
+            kv_heads=token_to_kv_pool.kv_heads,
+            head_dim=token_to_kv_pool.head_dim,
+        )
+        self._skip_first_decode_update = torch.zeros(req_to_token_pool.size, dtype=torch.bool, device=device)
+        self._positions = torch.empty((req_to_token_pool.size, cfg.top_k), dtype=torch.int32, device=device)
+        self._attn_ws = AttentionWorkspace(device)
+
+    # ---------------------------------------------------------------- per step
+
+    def init_forward_metadata(self, batch: ForwardBatch) -> None:
+        if batch.forward_mode.is_decode():
+            self._do_quest_decode_step_update(batch.req_pool_indices, batch.seq_lens)
+            self.quest.prepare_step(batch.seq_lens)
+
+    def _do_quest_decode_step_update(self, req_pool_indices: torch.Tensor, seq_lens: torch.Tensor) -> None:
+        """[Q3] The previous step's token sits at position ``seq_len - 2`` (quest_only.py:84-97).
+
+        Requests on their first decode step after prefill get row -1, which the
+        fused kernel skips (no fold, no counter advance), without a host sync.
+        """
+        dev = self.quest.device
+        rpi = req_pool_indices.to(device=dev, dtype=torch.int64)
+        seq = seq_lens.to(device=dev, dtype=torch.int64)
+        skip = self._skip_first_decode_update[rpi]
+        self._skip_first_decode_update.index_fill_(0, rpi, False)  # no host copy: graph-capturable
+        prev = (seq - 2).clamp(min=0)
+        locs = self.req_to_token[rpi, prev].to(torch.int64)
+        locs = torch.where(skip, torch.full_like(locs, -1), locs)
+        self.quest.update_decode_representations_fused(rpi, self.token_to_kv_pool.k_all, locs)
+
+    # ----------------------------------------------------------------- prefill
+
+    def forward_extend(self, q, k, v, layer, batch: ForwardBatch) -> torch.Tensor:
+        out = super().forward_extend(q, k, v, layer, batch)
+        if layer.layer_id == self.quest.end_layer - 1:
+            self._update_quest_for_extend(batch)
+        return out
+
+    def _update_quest_for_extend(self, batch: ForwardBatch) -> None:
+        """[Q2] Per request: bounds of positions ``0 .. seq_len-1`` at every layer (quest_only.py:115-128)."""
+        for req_idx, seq_len in zip(batch.req_pool_indices.tolist(), batch.seq_lens.tolist(), strict=True):
+            prefill_indices = self.req_to_token[req_idx, :seq_len]
+            self.quest.update_prefill_representations_fused(req_idx, self.token_to_kv_pool.k_all, prefill_indices)
+            self._skip_first_decode_update[req_idx] = True
+
+    # ------------------------------------------------------------------ decode
+
+    def forward_decode(self, q, k, v, layer, batch: ForwardBatch) -> torch.Tensor:
+        """quest_only.py:132-159: save K/V, select, then gather + attend in one kernel."""
+        assert batch.out_cache_loc is not None
+        self.token_to_kv_pool.set_kv_buffer(layer.layer_id, batch.out_cache_loc, k, v)
+        bs = batch.batch_size
+        positions, actual = self.quest.retrieve_topk(
+            q, layer.layer_id, batch.req_pool_indices, batch.seq_lens, out=self._positions
+        )
+        return self.sparse_attention(q, layer, batch.req_pool_indices, positions, actual, bs)
+
+    def sparse_attention(self, q, layer, req_pool_indices, positions, actual, bs) -> torch.Tensor:
+        """[Q7] rows = req_to_token[req, positions[:n]] -> attention over exactly those rows."""
+        heads = q.shape[1] if q.dim() == 3 else q.shape[1] // self.token_to_kv_pool.head_dim
+        dim = self.token_to_kv_pool.head_dim
+        q3 = q.reshape(bs, heads, dim).contiguous()
+        k_buf, v_buf = self.token_to_kv_pool.get_kv_buffer(layer.layer_id)
+        rpi = req_pool_indices
+        if rpi.dtype != torch.int64 or rpi.device != q3.device:
+            rpi = rpi.to(device=q3.device, dtype=torch.int64)
+        rpi = rpi.contiguous()
+        buf, tickets = self._attn_ws.get(bs, positions.shape[1], heads, dim)
+        out = torch.empty((bs, heads * dim), dtype=q3.dtype, device=q3.device)
+        r2t = self.req_to_token
+        _lib.call(
+            "qq_quest_decode_attention", _lib.ptr(q3), _lib.dtype_code(q3.dtype), q3.stride(0), heads,
+            _lib.ptr(k_buf), _lib.ptr(v_buf), _lib.dtype_code(k_buf.dtype), k_buf.shape[0],
+            self.token_to_kv_pool.kv_heads, dim, _lib.ptr(r2t), r2t.stride(0), r2t.shape[0], _lib.ptr(rpi),
+            _lib.ptr(positions), positions.stride(0), _lib.ptr(actual), bs, float(layer.scaling),
+            _lib.ptr(out), _lib.ptr(buf), buf.numel(), _lib.ptr(tickets), _lib.stream(q3.device),
+        )
+        return out
+
+    # --------------------------------------------------------------- lifecycle
+
+    def on_request_finished(self, req_pool_idx: int) -> None:
+        """[Q8] quest_only.py:163-167."""
+        self.quest.invalidate_request(req_pool_idx)
+        self._skip_first_decode_update[req_pool_idx] = False

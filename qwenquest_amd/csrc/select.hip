@@ -1,0 +1,425 @@
+// Quest page scoring + top-k page selection + token layout, one launch per layer.
+//
+// Reference: src/qwenquest/quest.py:366-464 (group_queries, page_scores,
+// retrieve_topk) and the layout of prepare_step (quest.py:333-342).
+//
+// Grid (blocks_per_request, bs).  Each block averages q over the GQA group,
+// then its 4 waves score pages: lane l holds channels [l*m, l*m + m) of the
+// page (m = ceil(KV*D / 64)), so a wave reads one page's KV*D (min, max) words
+// as one coalesced 2 KiB stream at KV*D = 512.  Per page the lane adds its m
+// fp32 products in channel order and the 64 lane sums are combined by a
+// halving tree (acc[l] += acc[l + w], w = 32 .. 1) - the canonical order the
+// oracle reproduces.  The last block of a request to finish (agent-scope
+// ticket) selects the top k = top_k/P - 1 pages with a 4-pass radix select on
+// order-preserving 32-bit keys, breaks ties at the threshold by lowest page
+// index, ranks the k winners by (score desc, page asc) and writes the
+// positions.  Short requests (seq <= top_k) only get the dense layout.
+#include "qq_common.h"
+
+namespace qq {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+constexpr int kMaxC = 1024;    // KV * D
+constexpr int kMaxSel = 1024;  // top_k / P - 1
+constexpr int kPagesPerBlock = 32;
+
+struct SelectArgs {
+  const void* q;
+  int q_dtype;
+  int64_t q_bstride;
+  int H;
+  const uint32_t* bounds_layer;  // [R, MP, C] (min, max) words of this layer
+  const int64_t* rpi;
+  const int64_t* seq;
+  const int32_t* limit;
+  int R, MP, KV, D, C, m, P, top_k, k_sel, ppb;
+  float* scores;
+  int32_t* tickets;
+  int32_t* positions;
+};
+
+__device__ inline void write_recent(int32_t* pos, int64_t s, int P) {
+  const int64_t start = max(s - P, (int64_t)0);
+  for (int j = threadIdx.x; j < P; j += kThreads) pos[j] = (int32_t)min(start + j, s - 1);
+}
+
+// Block-wide inclusive suffix sum over 256 entries of `v` (in place).
+__device__ inline void suffix_sum_256(uint32_t* v) {
+  const int t = threadIdx.x;
+  for (int off = 1; off < 256; off <<= 1) {
+    __syncthreads();
+    const uint32_t add = (t + off < 256) ? v[t + off] : 0u;
+    __syncthreads();
+    v[t] += add;
+  }
+  __syncthreads();
+}
+
+// Block-wide exclusive prefix sum over 256 entries (in place).
+__device__ inline void prefix_sum_256_exclusive(int* v) {
+  const int t = threadIdx.x;
+  const int mine = v[t];
+  for (int off = 1; off < 256; off <<= 1) {
+    __syncthreads();
+    const int add = (t >= off) ? v[t - off] : 0;
+    __syncthreads();
+    v[t] += add;
+  }
+  __syncthreads();
+  v[t] -= mine;
+  __syncthreads();
+}
+
+// GQA mean of channel c = h*D + d (quest.py:385-391): fp32 sum over the G query
+// heads of KV head h in head order, divided by G, rounded once to the query
+// dtype.  G == 1 returns the query unchanged.
+__device__ inline float gqa_mean(const void* q, int dtype, int64_t qb, int G, int D, int c) {
+  if (G == 1) return load_as_float(q, qb + c, dtype);
+  const int h = c / D, d = c - h * D;
+  float acc = 0.0f;
+  for (int g = 0; g < G; ++g)
+    acc = __fadd_rn(acc, load_as_float(q, qb + (int64_t)(h * G + g) * D + d, dtype));
+  acc = acc / (float)G;
+  return dtype == QQ_DTYPE_BF16 ? bf2f(f2bf(acc)) : acc;
+}
+
+// Lane `lane` adds channels lane*m .. lane*m + m - 1 (m <= M, channels >= C count
+// as +0.0), then the 64 lane sums are combined by the halving tree.
+template <int M>
+__device__ inline float score_page(const uint32_t* pb, const float* qreg, int lane, int m, int C) {
+  uint32_t w[M];
+  if (M % 4 == 0 && m == M && C == 64 * M) {
+    const uint4* p4 = reinterpret_cast<const uint4*>(pb + lane * M);
+#pragma unroll
+    for (int i = 0; i < M / 4; ++i) {
+      const uint4 v = p4[i];
+      w[4 * i + 0] = v.x;
+      w[4 * i + 1] = v.y;
+      w[4 * i + 2] = v.z;
+      w[4 * i + 3] = v.w;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < M; ++j) {
+      const int c = lane * m + j;
+      w[j] = (j < m && c < C) ? pb[c] : 0u;
+    }
+  }
+  float acc = 0.0f;
+#pragma unroll
+  for (int j = 0; j < M; ++j) {
+    const int c = lane * m + j;
+    const float qv = qreg[j];
+    const float kv = qv >= 0.0f ? bf2f((uint16_t)(w[j] >> 16)) : bf2f((uint16_t)(w[j] & 0xFFFFu));
+    const float prod = (j < m && c < C) ? __fmul_rn(qv, kv) : 0.0f;
+    if (j == 0)
+      acc = prod;
+    else if (j < m)
+      acc = __fadd_rn(acc, prod);
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) acc = __fadd_rn(acc, __shfl_down(acc, off, 64));
+  return acc;
+}
+
+template <int M>
+__global__ __launch_bounds__(kThreads) void score_select_kernel(SelectArgs a) {
+  const int b = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int64_t s = a.seq[b];
+  int32_t* pos = a.positions + (int64_t)b * a.top_k;
+
+  if (s <= a.top_k) {  // dense layout, quest.py:339-342 / 460
+    if (blockIdx.x == 0)
+      for (int j = tid; j < a.top_k; j += kThreads)
+        pos[j] = (int32_t)min((int64_t)j, max(s - 1, (int64_t)0));
+    return;
+  }
+  const int k = a.k_sel;
+  if (k == 0) {  // top_k == P: the recent window is the whole layout (quest.py:457-458)
+    if (blockIdx.x == 0) write_recent(pos, s, a.P);
+    return;
+  }
+  const int lim = min(a.limit[b], a.MP);
+  const int n_eff = max(lim, k);
+  const int nblk = max(1, (lim + a.ppb - 1) / a.ppb);
+  if ((int)blockIdx.x >= nblk) return;
+
+  __shared__ float s_q[kMaxC];
+  __shared__ int s_last;
+  for (int c = tid; c < a.C; c += kThreads)
+    s_q[c] = gqa_mean(a.q, a.q_dtype, (int64_t)b * a.q_bstride, a.H / a.KV, a.D, c);
+  __syncthreads();
+
+  const int wave = tid >> 6, lane = tid & 63;
+  float qreg[M];
+#pragma unroll
+  for (int j = 0; j < M; ++j) {
+    const int c = lane * a.m + j;
+    qreg[j] = (j < a.m && c < a.C) ? s_q[c] : 0.0f;
+  }
+  const int64_t req = a.rpi[b];
+  const bool req_ok = req >= 0 && req < a.R;
+  const uint32_t* pbase = a.bounds_layer + (req_ok ? req : 0) * a.MP * a.C;
+  float* sc = a.scores + (int64_t)b * a.MP;
+  const int p0 = blockIdx.x * a.ppb;
+  const int p1 = req_ok ? min(p0 + a.ppb, lim) : p0;
+  for (int p = p0 + wave; p < p1; p += 2 * kWaves) {
+    const int p2 = p + kWaves;
+    const float s0 = score_page<M>(pbase + (int64_t)p * a.C, qreg, lane, a.m, a.C);
+    float s1 = 0.0f;
+    if (p2 < p1) s1 = score_page<M>(pbase + (int64_t)p2 * a.C, qreg, lane, a.m, a.C);
+    if (lane == 0) {
+      sc[p] = s0;
+      if (p2 < p1) sc[p2] = s1;
+    }
+  }
+
+  // ---- last block of this request selects (quest.py:450-460)
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  __syncthreads();
+  if (tid == 0) s_last = (ticket_arrive(&a.tickets[b]) == nblk - 1);
+  __syncthreads();
+  if (!s_last) return;
+  acquire_fence();
+
+  __shared__ uint32_t s_hist[256];
+  __shared__ uint32_t s_prefix, s_mask;
+  __shared__ int s_remaining;
+  __shared__ uint32_t s_sel_key[kMaxSel];
+  __shared__ int s_sel_idx[kMaxSel];
+  __shared__ int s_order[kMaxSel];
+  __shared__ int s_eq[256];
+  __shared__ int s_gt;
+  const uint32_t kNegInfKey = 0x007FFFFFu;  // orderable(-inf): masked pages (quest.py:451)
+  auto key_of = [&](int p) -> uint32_t {
+    return p < lim ? orderable(sc[p]) : kNegInfKey;
+  };
+  if (tid == 0) {
+    s_prefix = 0;
+    s_mask = 0;
+    s_remaining = k;
+    s_gt = 0;
+  }
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    __syncthreads();
+    const uint32_t prefix = s_prefix, mask = s_mask;
+    const int remaining = s_remaining;
+    s_hist[tid] = 0;
+    __syncthreads();
+    for (int p = tid; p < n_eff; p += kThreads) {
+      const uint32_t key = key_of(p);
+      if ((key & mask) == prefix) atomicAdd(&s_hist[(key >> shift) & 255u], 1u);
+    }
+    suffix_sum_256(s_hist);
+    const uint32_t here = s_hist[tid];
+    const uint32_t above = tid < 255 ? s_hist[tid + 1] : 0u;
+    __syncthreads();
+    if (here >= (uint32_t)remaining && above < (uint32_t)remaining) {
+      s_prefix = prefix | ((uint32_t)tid << shift);
+      s_mask = mask | (255u << shift);
+      s_remaining = remaining - (int)above;
+    }
+  }
+  __syncthreads();
+  const uint32_t thr = s_prefix;
+  const int ties = s_remaining;  // how many pages with key == thr to take
+  const int gt = k - ties;
+
+  // keys above the threshold (any order; ranked below), ties by lowest index
+  const int chunk = (n_eff + kThreads - 1) / kThreads;
+  const int lo = min(tid * chunk, n_eff), hi = min(lo + chunk, n_eff);
+  int eq = 0;
+  for (int p = lo; p < hi; ++p) {
+    const uint32_t key = key_of(p);
+    if (key > thr) {
+      const int slot = atomicAdd(&s_gt, 1);
+      s_sel_key[slot] = key;
+      s_sel_idx[slot] = p;
+    } else if (key == thr) {
+      ++eq;
+    }
+  }
+  s_eq[tid] = eq;
+  prefix_sum_256_exclusive(s_eq);
+  int rank = s_eq[tid];
+  for (int p = lo; p < hi && rank < ties; ++p) {
+    if (key_of(p) == thr) {
+      s_sel_key[gt + rank] = thr;
+      s_sel_idx[gt + rank] = p;
+      ++rank;
+    }
+  }
+  __syncthreads();
+  for (int i = tid; i < k; i += kThreads) {
+    const uint32_t ki = s_sel_key[i];
+    const int ii = s_sel_idx[i];
+    int r = 0;
+    for (int j = 0; j < k; ++j) {
+      const uint32_t kj = s_sel_key[j];
+      r += (kj > ki) || (kj == ki && s_sel_idx[j] < ii);
+    }
+    s_order[r] = ii;
+  }
+  __syncthreads();
+  const int P = a.P;
+  for (int slot = tid; slot < k * P; slot += kThreads) {
+    const int r = slot / P;
+    pos[slot] = s_order[r] * P + (slot - r * P);
+  }
+  write_recent(pos + (int64_t)k * P, s, P);
+  if (tid == 0) a.tickets[b] = 0;
+}
+
+// group_queries (quest.py:366-391) as its own kernel: out [bs, C] in q's dtype.
+__global__ __launch_bounds__(kThreads) void group_queries_kernel(const void* q, int dtype,
+                                                               int64_t bstride, int G, int D, int C,
+                                                               void* out) {
+  const int b = blockIdx.y;
+  for (int c = blockIdx.x * kThreads + threadIdx.x; c < C; c += gridDim.x * kThreads) {
+    const float v = gqa_mean(q, dtype, (int64_t)b * bstride, G, D, c);
+    if (dtype == QQ_DTYPE_BF16)
+      static_cast<uint16_t*>(out)[(int64_t)b * C + c] = f2bf(v);
+    else
+      static_cast<float*>(out)[(int64_t)b * C + c] = v;
+  }
+}
+
+// page_scores (quest.py:393-405) over every page slot [0, MP), canonical order.
+template <int M>
+__global__ __launch_bounds__(kThreads) void page_scores_kernel(const void* qbar, int dtype,
+                                                             int64_t bstride,
+                                                             const uint32_t* bounds_layer,
+                                                             const int64_t* rpi, int R, int MP,
+                                                             int C, int m, float* scores) {
+  const int b = blockIdx.y;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  float qreg[M];
+#pragma unroll
+  for (int j = 0; j < M; ++j) {
+    const int c = lane * m + j;
+    qreg[j] = (j < m && c < C) ? load_as_float(qbar, (int64_t)b * bstride + c, dtype) : 0.0f;
+  }
+  const int64_t req = rpi[b];
+  if (req < 0 || req >= R) return;
+  const uint32_t* pbase = bounds_layer + req * (int64_t)MP * C;
+  const int p0 = blockIdx.x * kPagesPerBlock;
+  const int p1 = min(p0 + kPagesPerBlock, MP);
+  for (int p = p0 + wave; p < p1; p += kWaves) {
+    const float sc = score_page<M>(pbase + (int64_t)p * C, qreg, lane, m, C);
+    if (lane == 0) scores[(int64_t)b * MP + p] = sc;
+  }
+}
+
+}  // namespace
+}  // namespace qq
+
+using namespace qq;
+
+extern "C" int qq_quest_group_queries(const void* q, int q_dtype, int64_t q_batch_stride,
+                                      int num_q_heads, int kv_heads, int head_dim, int bs,
+                                      void* out, void* stream) {
+  QQ_REQUIRE(dtype_ok(q_dtype), "qq_quest_group_queries: unsupported dtype %d", q_dtype);
+  QQ_REQUIRE(kv_heads > 0 && head_dim > 0 && num_q_heads > 0, "qq_quest_group_queries: bad heads");
+  QQ_REQUIRE(num_q_heads % kv_heads == 0, "q_heads %d not divisible by kv_heads %d", num_q_heads,
+             kv_heads);
+  if (bs == 0) return QQ_OK;
+  const int C = kv_heads * head_dim;
+  dim3 grid(ceil_div(C, kThreads), bs);
+  group_queries_kernel<<<grid, kThreads, 0, static_cast<hipStream_t>(stream)>>>(
+      q, q_dtype, q_batch_stride, num_q_heads / kv_heads, head_dim, C, out);
+  return check_launch("qq_quest_group_queries");
+}
+
+extern "C" int qq_quest_page_scores(const void* grouped_q, int q_dtype, int64_t q_batch_stride,
+                                    const uint16_t* page_k_bounds, int layer,
+                                    const int64_t* req_pool_indices, int bs, int max_reqs,
+                                    int max_pages, int kv_heads, int head_dim, float* scores,
+                                    void* stream) {
+  QQ_REQUIRE(dtype_ok(q_dtype), "qq_quest_page_scores: unsupported dtype %d", q_dtype);
+  const int C = kv_heads * head_dim;
+  QQ_REQUIRE(C > 0 && C <= kMaxC, "qq_quest_page_scores: kv_heads*head_dim %d unsupported", C);
+  if (bs == 0 || max_pages == 0) return QQ_OK;
+  const uint32_t* bl =
+      reinterpret_cast<const uint32_t*>(page_k_bounds) + (int64_t)layer * max_reqs * max_pages * C;
+  dim3 grid(ceil_div(max_pages, kPagesPerBlock), bs);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int m = (C + 63) / 64;
+  if (m <= 1)
+    page_scores_kernel<1><<<grid, kThreads, 0, s>>>(grouped_q, q_dtype, q_batch_stride, bl,
+                                                    req_pool_indices, max_reqs, max_pages, C, m, scores);
+  else if (m <= 2)
+    page_scores_kernel<2><<<grid, kThreads, 0, s>>>(grouped_q, q_dtype, q_batch_stride, bl,
+                                                    req_pool_indices, max_reqs, max_pages, C, m, scores);
+  else if (m <= 4)
+    page_scores_kernel<4><<<grid, kThreads, 0, s>>>(grouped_q, q_dtype, q_batch_stride, bl,
+                                                    req_pool_indices, max_reqs, max_pages, C, m, scores);
+  else if (m <= 8)
+    page_scores_kernel<8><<<grid, kThreads, 0, s>>>(grouped_q, q_dtype, q_batch_stride, bl,
+                                                    req_pool_indices, max_reqs, max_pages, C, m, scores);
+  else
+    page_scores_kernel<16><<<grid, kThreads, 0, s>>>(grouped_q, q_dtype, q_batch_stride, bl,
+                                                     req_pool_indices, max_reqs, max_pages, C, m, scores);
+  return check_launch("qq_quest_page_scores");
+}
+
+extern "C" int qq_quest_retrieve_topk(const void* q, int q_dtype, int64_t q_batch_stride,
+                                      int num_q_heads, const uint16_t* page_k_bounds, int layer,
+                                      const int64_t* req_pool_indices, const int64_t* seq_lens,
+                                      const int32_t* candidate_limit, int bs, int max_reqs,
+                                      int max_pages, int kv_heads, int head_dim, int page_size,
+                                      int top_k, float* scores_ws, int32_t* tickets,
+                                      int32_t* positions, void* stream) {
+  QQ_REQUIRE(dtype_ok(q_dtype), "qq_quest_retrieve_topk: unsupported query dtype %d", q_dtype);
+  QQ_REQUIRE(kv_heads > 0 && head_dim > 0 && num_q_heads > 0, "qq_quest_retrieve_topk: bad heads");
+  QQ_REQUIRE(num_q_heads % kv_heads == 0, "q_heads %d not divisible by kv_heads %d", num_q_heads,
+             kv_heads);
+  QQ_REQUIRE(page_size > 0 && top_k > 0 && top_k % page_size == 0,
+             "qq_quest_retrieve_topk: top_k %d must be a positive multiple of page_size %d", top_k,
+             page_size);
+  const int C = kv_heads * head_dim;
+  const int k_sel = top_k / page_size - 1;
+  QQ_REQUIRE(C <= kMaxC, "qq_quest_retrieve_topk: kv_heads*head_dim %d exceeds %d", C, kMaxC);
+  QQ_REQUIRE(k_sel <= kMaxSel, "qq_quest_retrieve_topk: %d selected pages exceed %d", k_sel, kMaxSel);
+  QQ_REQUIRE(bs >= 0 && layer >= 0 && max_pages >= 0, "qq_quest_retrieve_topk: bad sizes");
+  if (bs == 0) return QQ_OK;
+  SelectArgs a;
+  a.q = q;
+  a.q_dtype = q_dtype;
+  a.q_bstride = q_batch_stride;
+  a.H = num_q_heads;
+  a.bounds_layer =
+      reinterpret_cast<const uint32_t*>(page_k_bounds) + (int64_t)layer * max_reqs * max_pages * C;
+  a.rpi = req_pool_indices;
+  a.seq = seq_lens;
+  a.limit = candidate_limit;
+  a.R = max_reqs;
+  a.MP = max_pages;
+  a.KV = kv_heads;
+  a.D = head_dim;
+  a.C = C;
+  a.m = (C + 63) / 64;
+  a.P = page_size;
+  a.top_k = top_k;
+  a.k_sel = k_sel;
+  a.ppb = kPagesPerBlock;
+  a.scores = scores_ws;
+  a.tickets = tickets;
+  a.positions = positions;
+  dim3 grid(max(1, ceil_div(max_pages, kPagesPerBlock)), bs);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int M = (C + 63) / 64;
+  if (M <= 1)
+    score_select_kernel<1><<<grid, kThreads, 0, s>>>(a);
+  else if (M <= 2)
+    score_select_kernel<2><<<grid, kThreads, 0, s>>>(a);
+  else if (M <= 4)
+    score_select_kernel<4><<<grid, kThreads, 0, s>>>(a);
+  else if (M <= 8)
+    score_select_kernel<8><<<grid, kThreads, 0, s>>>(a);
+  else
+    score_select_kernel<16><<<grid, kThreads, 0, s>>>(a);
+  return check_launch("qq_quest_retrieve_topk");
+}

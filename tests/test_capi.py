@@ -1,0 +1,88 @@
+"""The C-ABI library loads, exports every symbol the header declares with the
+argument count the ctypes binding uses, and reports argument errors - all
+without a GPU (no kernel is launched)."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from tests.conftest import ROOT
+
+HEADER = os.path.join(ROOT, "include", "qwenquest_amd.h")
+
+
+def _declarations() -> dict[str, int]:
+    """name -> number of parameters, parsed from include/qwenquest_amd.h."""
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    decls = {}
+    for m in re.finditer(r"\b(?:int|int64_t|const char\*)\s+(qq_\w+)\s*\(([^)]*)\)\s*;", text):
+        params = [p for p in m.group(2).split(",") if p.strip() and p.strip() != "void"]
+        decls[m.group(1)] = len(params)
+    return decls
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from qwenquest_amd import _lib
+
+    if not os.path.exists(_lib.LIB_PATH):
+        from qwenquest_amd import build
+
+        build.build()
+    return _lib.load()
+
+
+def test_header_declares_the_entry_points():
+    decls = _declarations()
+    assert len(decls) >= 12
+    for name in ("qq_quest_retrieve_topk", "qq_quest_decode_attention", "qq_quest_prefill_bounds"):
+        assert name in decls
+
+
+def test_every_declared_symbol_is_exported_with_matching_arity(lib):
+    from qwenquest_amd import _lib
+
+    decls = _declarations()
+    for name, nargs in decls.items():
+        assert hasattr(lib, name), f"{name} not exported"
+        assert name in _lib.SIGNATURES, f"{name} missing from the ctypes binding"
+        assert len(_lib.SIGNATURES[name][1]) == nargs, f"{name}: binding arity != header"
+    assert set(_lib.SIGNATURES) == set(decls)
+
+
+def test_version_and_error_mapping_without_gpu(lib):
+    from qwenquest_amd import _lib
+
+    assert lib.qq_version() == 100
+    # argument validation happens before any HIP call: page_size 0 -> QQ_EINVAL
+    st = lib.qq_quest_prepare_step(None, 1, 0, 64, 0, None, None, None)
+    assert st == _lib.QQ_EINVAL
+    assert b"bad arguments" in lib.qq_last_error()
+    with pytest.raises(ValueError):
+        _lib.check(st)
+    st = lib.qq_quest_retrieve_topk(None, 0, 0, 32, None, 0, None, None, None, 1, 1, 1, 4, 128,
+                                    64, 100, None, None, None, None)
+    assert st == _lib.QQ_EINVAL and b"multiple" in lib.qq_last_error()
+    assert lib.qq_decode_attention_workspace_bytes(16, 2048, 32, 128) == 16 * 32 * 32 * 130 * 4
+
+
+def test_cpu_tensors_are_refused():
+    import torch
+
+    from qwenquest_amd import _lib
+
+    with pytest.raises(RuntimeError, match="GPU only"):
+        _lib.ptr(torch.zeros(4))
+
+
+def test_library_has_no_host_fallback_symbols(lib):
+    """Every exported qq_ symbol is one the header declares (nothing undocumented)."""
+    out = os.popen(f"nm -D --defined-only {lib._name}").read()
+    exported = set(re.findall(r"\b(qq_\w+)\b", out))
+    assert exported == set(_declarations())
+    assert ctypes.sizeof(ctypes.c_void_p) == 8

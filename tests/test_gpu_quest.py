@@ -1,0 +1,403 @@
+"""GPU parity of the Quest path (bounds, GQA mean, scores, selection, attention)
+against the CPU oracle on identical seeded inputs.
+
+Bounds, scores (canonical order), positions: bit-exact.  Attention: 2e-2 abs
+in bf16, 1e-4 abs in fp32 (the tolerances stated for the path).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as oa
+from oracle import bf16
+from oracle import quest as oq
+from tests.conftest import bf16_bits, load_golden
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda", 0)
+
+
+def rand_bf16(shape, seed, scale=1.0, mean=None):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(*shape, generator=g) * scale
+    if mean is not None:
+        x = x + mean
+    return x.to(torch.bfloat16)
+
+
+def new_quest(top_k, page, layers, reqs, ctx, kv, d, avoid=False):
+    from qwenquest_amd.quest import QuestAlgorithm
+
+    q = QuestAlgorithm(top_k=top_k, page_size=page, device=DEV, avoid_recent_overlap=avoid)
+    q.init_storage(0, layers, reqs, ctx, kv, d)
+    st = oq.QuestState(top_k, page, avoid_recent_overlap=avoid)
+    st.init_storage(0, layers, reqs, ctx, kv, d)
+    return q, st
+
+
+def assert_state_equal(q, st):
+    torch.cuda.synchronize()
+    assert np.array_equal(bf16_bits(q.page_k_bounds), st.page_k_bounds)
+    assert np.array_equal(bf16_bits(q.running_k_min), st.running_k_min)
+    assert np.array_equal(bf16_bits(q.running_k_max), st.running_k_max)
+    assert np.array_equal(q.running_token_count.cpu().numpy(), st.running_token_count)
+    assert np.array_equal(q.running_page_idx.cpu().numpy(), st.running_page_idx)
+
+
+# ------------------------------------------------------------------ bounds
+
+
+def test_init_storage_sentinels_match_oracle():
+    q, st = new_quest(256, 64, 2, 3, 1000, 4, 32)
+    assert_state_equal(q, st)
+    assert not q.page_valid.any()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("n", [0, 30, 64, 192, 200, 777])
+def test_prefill_bounds_bit_exact(dtype, n):
+    q, st = new_quest(256, 64, 2, 4, 1024, 4, 32)
+    pool = rand_bf16((1100, 4, 32), seed=n).to(dtype)
+    idx = torch.randperm(1100, generator=torch.Generator().manual_seed(1))[:n].to(torch.int32)
+    host = pool.float().numpy() if dtype == torch.float32 else bf16_bits(pool)
+    for layer in range(2):
+        q.update_prefill_representations(layer, 2, pool.to(DEV), idx.to(DEV))
+        st.update_prefill_representations(layer, 2, host, idx.numpy())
+    assert_state_equal(q, st)
+
+
+def test_prefill_fused_over_layers_equals_per_layer():
+    from qwenquest_amd.memory import MHATokenToKVPool
+
+    kvp = MHATokenToKVPool(600, 3, 2, 16, torch.bfloat16, DEV)
+    kvp.k_all.copy_(rand_bf16((3, 601, 2, 16), seed=3).to(DEV))
+    idx = torch.arange(1, 517, device=DEV)
+    a, _ = new_quest(64, 16, 3, 2, 600, 2, 16)
+    b, _ = new_quest(64, 16, 3, 2, 600, 2, 16)
+    a.update_prefill_representations_fused(1, kvp.k_all, idx)
+    for layer in range(3):
+        b.update_prefill_representations(layer, 1, kvp.k_buffer[layer], idx)
+    torch.cuda.synchronize()
+    assert torch.equal(a.page_k_bounds, b.page_k_bounds)
+    assert torch.equal(a.running_k_min, b.running_k_min)
+    assert torch.equal(a.running_token_count, b.running_token_count)
+
+
+@pytest.mark.parametrize("fused", [False, True])
+def test_decode_fold_and_finalize_bit_exact_across_page_boundaries(fused):
+    from qwenquest_amd.memory import MHATokenToKVPool
+
+    L, KV, D, P = 2, 4, 32, 16
+    kvp = MHATokenToKVPool(400, L, KV, D, torch.bfloat16, DEV)
+    kvp.k_all.copy_(rand_bf16((L, 401, KV, D), seed=5).to(DEV))
+    host = bf16_bits(kvp.k_all.cpu())
+    q, st = new_quest(64, P, L, 3, 400, KV, D)
+    for r, n in ((0, 50), (2, 64)):
+        q.update_prefill_representations_fused(r, kvp.k_all, torch.arange(1 + 100 * r, 1 + 100 * r + n, device=DEV))
+        for layer in range(L):
+            st.update_prefill_representations(layer, r, host[layer], np.arange(1 + 100 * r, 1 + 100 * r + n))
+    reqs = torch.tensor([0, 2], device=DEV)
+    for step in range(40):
+        locs = torch.tensor([1 + 50 + step, 201 + 64 + step], device=DEV)
+        if fused:
+            q.update_decode_representations_fused(reqs, kvp.k_all, locs)
+        else:
+            for layer in range(L):
+                q.update_decode_representations(layer, reqs, kvp.k_buffer[layer], locs)
+            q.maybe_finalize_decode_representations(reqs)
+        for layer in range(L):
+            st.update_decode_representations(layer, [0, 2], host[layer], locs.cpu().numpy())
+        st.maybe_finalize_decode_representations([0, 2])
+    assert_state_equal(q, st)
+    assert q.page_valid[:, 0, :5].all() and not q.page_valid[:, 0, 5:].any()
+
+
+def test_decode_skip_rows_are_left_untouched():
+    from qwenquest_amd.memory import MHATokenToKVPool
+
+    kvp = MHATokenToKVPool(100, 1, 2, 8, torch.bfloat16, DEV)
+    kvp.k_all.copy_(rand_bf16((1, 101, 2, 8), seed=6).to(DEV))
+    q, _ = new_quest(16, 4, 1, 2, 64, 2, 8)
+    q.update_prefill_representations_fused(0, kvp.k_all, torch.arange(1, 4, device=DEV))
+    before = (q.running_k_min.clone(), q.running_token_count.clone())
+    q.update_decode_representations_fused(torch.tensor([0], device=DEV), kvp.k_all, torch.tensor([-1], device=DEV))
+    torch.cuda.synchronize()
+    assert torch.equal(before[0], q.running_k_min) and torch.equal(before[1], q.running_token_count)
+
+
+def test_invalidate_request_resets_one_slot():
+    q, st = new_quest(64, 16, 2, 4, 512, 4, 32)
+    pool = rand_bf16((512, 4, 32), seed=7)
+    for r in (1, 2, 3):
+        for layer in range(2):
+            q.update_prefill_representations(layer, r, pool.to(DEV), torch.arange(150, device=DEV))
+            st.update_prefill_representations(layer, r, bf16_bits(pool), np.arange(150))
+    q.invalidate_request(2)
+    st.invalidate_request(2)
+    assert_state_equal(q, st)
+
+
+# ----------------------------------------------------------- GQA mean + scores
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("heads,kv", [(32, 4), (16, 4), (4, 4), (8, 2)])
+def test_group_queries_bit_exact(dtype, heads, kv):
+    from qwenquest_amd.quest import QuestAlgorithm
+
+    d = 32
+    quest = QuestAlgorithm(top_k=64, page_size=16, device=DEV)
+    quest.init_storage(0, 1, 1, 64, kv, d)
+    qv = rand_bf16((5, heads, d), seed=heads).to(dtype)
+    got = quest.group_queries(qv.to(DEV)).float().cpu().numpy()
+    ref = oq.group_queries(qv.float().numpy(), kv, d, is_bf16=dtype == torch.bfloat16)
+    assert np.array_equal(got, ref)
+
+
+@pytest.mark.parametrize("kv,d", [(4, 128), (4, 32), (2, 8), (5, 32), (8, 128), (1, 24)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_page_scores_bit_exact_in_canonical_order(kv, d, dtype):
+    P = 8
+    q, st = new_quest(32, P, 1, 2, 512, kv, d)
+    pool = rand_bf16((512, kv, d), seed=kv * d)
+    q.update_prefill_representations(0, 1, pool.to(DEV), torch.arange(400, device=DEV))
+    st.update_prefill_representations(0, 1, bf16_bits(pool), np.arange(400))
+    qbar = (rand_bf16((3, kv, d), seed=9) * 3).to(dtype)
+    got = q.page_scores(qbar.to(DEV), 0, torch.tensor([1, 1, 0], device=DEV)).cpu().numpy()
+    ref = oq.page_scores(qbar.float().numpy(), st.page_k_bounds[0, [1, 1, 0]])
+    assert np.array_equal(got.view(np.uint32), (ref + np.float32(0)).view(np.uint32)) or np.array_equal(got, ref)
+    assert np.array_equal(np.isneginf(got), np.isneginf(ref))
+
+
+# ------------------------------------------------------------------ selection
+
+
+def run_retrieve(q, st, queries, reqs, seqs, layer=0):
+    seq_t = torch.tensor(seqs, device=DEV)
+    q.prepare_step(seq_t)
+    pos, actual = q.retrieve_topk(queries.to(DEV), layer, torch.tensor(reqs, device=DEV), seq_t)
+    st.prepare_step(seqs)
+    ref_pos, ref_actual, _ = st.retrieve_topk(queries.float().numpy(), layer, reqs,
+                                              q_is_bf16=queries.dtype == torch.bfloat16)
+    pos, actual = pos.cpu().numpy(), actual.cpu().numpy()
+    assert np.array_equal(actual, ref_actual)
+    for i in range(len(seqs)):
+        n = int(actual[i])
+        assert np.array_equal(pos[i, :n], ref_pos[i, :n]), f"request {i} seq {seqs[i]}"
+    return pos, actual
+
+
+@pytest.mark.parametrize("avoid", [False, True])
+@pytest.mark.parametrize("top_k,P,heads", [(256, 64, 4), (128, 16, 16), (64, 16, 32), (32, 8, 8), (16, 16, 4)])
+def test_retrieve_topk_positions_bit_exact(avoid, top_k, P, heads):
+    kv, d = 4, 32
+    q, st = new_quest(top_k, P, 2, 4, 2048, kv, d, avoid)
+    pool = rand_bf16((2048, kv, d), seed=top_k + P)
+    lens = (2000, 800, top_k, 300)
+    for r, n in enumerate(lens):
+        for layer in range(2):
+            q.update_prefill_representations(layer, r, pool.to(DEV), torch.arange(n, device=DEV))
+            st.update_prefill_representations(layer, r, bf16_bits(pool), np.arange(n))
+    for dtype in (torch.bfloat16, torch.float32):
+        queries = rand_bf16((4, heads, d), seed=heads).to(dtype)
+        run_retrieve(q, st, queries, [0, 1, 2, 3], [2001, 801, top_k, 301], layer=1)
+        run_retrieve(q, st, queries[:2], [3, 0], [300 + P, 1999])
+
+
+def test_retrieve_topk_ties_break_to_lowest_page():
+    q, st = new_quest(256, 64, 1, 1, 2048, 4, 32)
+    pool = torch.zeros(2048, 4, 32, dtype=torch.bfloat16)
+    pool[320:384] = 5.0
+    q.update_prefill_representations(0, 0, pool.to(DEV), torch.arange(640, device=DEV))
+    st.update_prefill_representations(0, 0, bf16_bits(pool), np.arange(640))
+    pos, _ = run_retrieve(q, st, torch.ones(1, 4, 32), [0], [640])
+    assert pos[0, :192].tolist() == list(range(320, 384)) + list(range(0, 128))
+
+
+def test_recent_window_overlap_known_answer():
+    pool = torch.zeros(2048, 4, 32, dtype=torch.bfloat16)
+    pool[48:64] = 3.0
+    for avoid in (False, True):
+        q, st = new_quest(32, 16, 1, 1, 2048, 4, 32, avoid)
+        q.update_prefill_representations(0, 0, pool.to(DEV), torch.arange(70, device=DEV))
+        st.update_prefill_representations(0, 0, bf16_bits(pool), np.arange(70))
+        pos, actual = run_retrieve(q, st, torch.ones(1, 4, 32), [0], [70])
+        if avoid:
+            assert len(set(pos[0].tolist())) == 32 and pos[0, -16:].tolist() == list(range(54, 70))
+        else:
+            assert set(range(54, 64)) <= set(pos[0, :16].tolist())
+
+
+def test_large_selection_count_and_stale_bounds():
+    """top_k / P - 1 = 255 selected pages (page size 1) and stale bounds past seq_len."""
+    q, st = new_quest(256, 1, 1, 2, 1024, 2, 16)
+    pool = rand_bf16((1024, 2, 16), seed=11)
+    for r in range(2):
+        q.update_prefill_representations(0, r, pool.to(DEV), torch.arange(1000, device=DEV))
+        st.update_prefill_representations(0, r, bf16_bits(pool), np.arange(1000))
+    run_retrieve(q, st, rand_bf16((2, 8, 16), seed=12), [0, 1], [1001, 600])
+
+
+def test_outlier_channels_stress_ties_and_overflow():
+    """Keys with x10 outlier channels and huge queries (sentinel pages -> -inf scores)."""
+    kv, d = 4, 128
+    pool = rand_bf16((4096, kv, d), seed=13).float()
+    pool[:, :, :4] *= 10
+    pool = pool.to(torch.bfloat16)
+    for avoid in (False, True):
+        q, st = new_quest(2048, 64, 1, 2, 4200, kv, d, avoid)
+        q.update_prefill_representations(0, 0, pool.to(DEV), torch.arange(4000, device=DEV))
+        st.update_prefill_representations(0, 0, bf16_bits(pool), np.arange(4000))
+        queries = rand_bf16((2, 32, d), seed=14, scale=50)
+        run_retrieve(q, st, queries, [0, 1], [4090, 2100])
+
+
+def test_golden_c1_selection_through_the_kernel():
+    """The reference's own positions (tests/golden, C1 shape): identical page sets."""
+    from qwenquest_amd.quest import QuestAlgorithm
+
+    g = load_golden("c1_selection.npz")
+    queries = torch.from_numpy(g["queries"].view(np.int16)).view(torch.bfloat16)
+    agree = 0
+    for avoid in (0, 1):
+        quest = QuestAlgorithm(top_k=2048, page_size=64, device=DEV, avoid_recent_overlap=bool(avoid))
+        quest.init_storage(0, 1, 16, 8192, 4, 128)
+        b = torch.from_numpy(g["bounds"].view(np.int16)).view(torch.bfloat16).to(DEV)
+        quest.page_k_bounds[0].copy_(b.expand(16, *b.shape))
+        for si, s in enumerate(g["seq_lens"].tolist()):
+            seq = torch.full((16,), s, device=DEV)
+            quest.prepare_step(seq)
+            pos, actual = quest.retrieve_topk(queries.to(DEV), 0, torch.arange(16, device=DEV), seq)
+            pos = pos.cpu().numpy()
+            ref = g[f"positions_avoid{avoid}"][si]
+            for i in range(16):
+                n = int(actual[i])
+                if s <= 2048:
+                    assert np.array_equal(pos[i, :n], ref[i, :n])
+                else:
+                    assert sorted(pos[i, :1984:64].tolist()) == sorted(ref[i, :1984:64].tolist())
+                    assert np.array_equal(pos[i, 1984:], ref[i, 1984:])
+                    agree += 1
+    assert agree == 160
+
+
+# ------------------------------------------------------------------ attention
+
+
+def attention_case(dtype, heads, kv, d, n_rows, seed, dup=False):
+    from qwenquest_amd.attention.ops import decode_attention_rows
+
+    pool = 3000
+    k = rand_bf16((pool, kv, d), seed=seed).to(dtype)
+    v = rand_bf16((pool, kv, d), seed=seed + 1).to(dtype)
+    q = rand_bf16((len(n_rows), heads, d), seed=seed + 2).to(dtype)
+    width = max(n_rows)
+    gen = torch.Generator().manual_seed(seed)
+    rows = torch.randint(0, pool, (len(n_rows), width), generator=gen)
+    if dup:
+        rows[:, 1] = rows[:, 0]
+    actual = torch.tensor(n_rows, dtype=torch.int32)
+    out = decode_attention_rows(q.to(DEV), k.to(DEV), v.to(DEV), rows.to(DEV), actual.to(DEV), d**-0.5)
+    ref = oa.sparse_decode(q.float().numpy(), k.float().numpy(), v.float().numpy(),
+                           [rows[i, :n].numpy() for i, n in enumerate(n_rows)], d**-0.5)
+    return out.float().cpu().numpy(), ref
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.bfloat16, 2e-2), (torch.float32, 1e-4)])
+@pytest.mark.parametrize("heads,kv,d", [(32, 4, 128), (8, 2, 16), (16, 4, 32), (4, 4, 8)])
+def test_attention_matches_oracle(dtype, tol, heads, kv, d):
+    out, ref = attention_case(dtype, heads, kv, d, [2048, 1, 65, 700], seed=heads + d, dup=True)
+    assert np.abs(out - ref).max() < tol
+
+
+def test_decode_attention_single_request_api():
+    from qwenquest_amd.attention.ops import decode_attention
+
+    q = rand_bf16((8, 16), seed=1).float()
+    k = rand_bf16((40, 2, 16), seed=2).float()
+    v = rand_bf16((40, 2, 16), seed=3).float()
+    rows = [0, 1, 2, 2, 39]
+    out = decode_attention(q.to(DEV), k[rows].to(DEV), v[rows].to(DEV), 0.25).cpu().numpy()
+    ref = oa.decode_attention(q.numpy(), k[rows].numpy(), v[rows].numpy(), 0.25)
+    assert np.abs(out - ref).max() < 1e-5
+
+
+# ------------------------------------------------------------ full backend
+
+
+def test_quest_backend_decode_steps_match_oracle():
+    """QuestOnlyBackend over 70 decode steps (pages complete and get selected) vs the oracle."""
+    from qwenquest_amd.attention.quest_only import QuestOnlyBackend
+    from qwenquest_amd.batch import ForwardBatch, ForwardMode
+    from qwenquest_amd.memory import MHATokenToKVPool, ReqToTokenPool
+
+    L, H, KV, D, P, TOP_K, CTX = 2, 8, 2, 16, 8, 32, 256
+    rtp = ReqToTokenPool(3, CTX, DEV)
+    kvp = MHATokenToKVPool(3 * CTX, L, KV, D, torch.bfloat16, DEV)
+    be = QuestOnlyBackend(rtp, kvp, {"algorithm": "quest", "top_k": TOP_K, "quest_page_size": P})
+    st = oq.QuestState(TOP_K, P)
+    st.init_storage(0, L, 3, CTX, KV, D)
+    kk = rand_bf16((L, 3 * CTX + 1, KV, D), seed=21)
+    vv = rand_bf16((L, 3 * CTX + 1, KV, D), seed=22)
+    kb, vb = bf16.to_f32(bf16_bits(kk)), bf16.to_f32(bf16_bits(vv))
+    kvp.k_all.copy_(kk.to(DEV))
+    kvp.v_all.copy_(vv.to(DEV))
+    prompt = {0: 45, 2: 20}
+    for r, n in prompt.items():
+        rtp.req_to_token[r] = torch.arange(1 + r * CTX, 1 + (r + 1) * CTX, dtype=torch.int32)
+        be.quest.update_prefill_representations_fused(r, kvp.k_all, rtp.req_to_token[r, :n])
+        be._skip_first_decode_update[r] = True
+        for layer in range(L):
+            st.update_prefill_representations(layer, r, bf16_bits(kk[layer]), np.arange(1 + r * CTX, 1 + r * CTX + n))
+    reqs = [0, 2]
+    first = {0: True, 2: True}
+
+    class Layer:
+        def __init__(self, i):
+            self.layer_id, self.scaling = i, D**-0.5
+
+    for step in range(70):
+        seqs = [prompt[r] + step + 1 for r in reqs]
+        batch = ForwardBatch(ForwardMode.DECODE, None, None, torch.tensor(reqs, device=DEV),
+                             torch.tensor(seqs, device=DEV), None, rtp, kvp, be)
+        be.init_forward_metadata(batch)
+        active = [r for r in reqs if not first[r]]
+        for r in reqs:
+            first[r] = False
+        if active:
+            for layer in range(L):
+                locs = [1 + r * CTX + prompt[r] + step - 1 for r in active]
+                st.update_decode_representations(layer, active, bf16_bits(kk[layer]), locs)
+            st.maybe_finalize_decode_representations(active)
+        st.prepare_step(seqs)
+        q = rand_bf16((2, H, D), seed=100 + step)
+        for layer in range(L):
+            pos, actual = be.quest.retrieve_topk(q.to(DEV), layer, batch.req_pool_indices, batch.seq_lens)
+            out = be.sparse_attention(q.to(DEV), Layer(layer), batch.req_pool_indices, pos, actual, 2)
+            ref_pos, ref_actual, _ = st.retrieve_topk(q.float().numpy(), layer, reqs)
+            pos = pos.cpu().numpy()
+            for i, r in enumerate(reqs):
+                n = int(ref_actual[i])
+                assert np.array_equal(pos[i, :n], ref_pos[i, :n]), f"step {step} layer {layer} req {r}"
+            rows = [1 + r * CTX + ref_pos[i, : int(ref_actual[i])] for i, r in enumerate(reqs)]
+            ref = oa.sparse_decode(q.float().numpy(), kb[layer], vb[layer], rows, D**-0.5)
+            assert np.abs(out.float().cpu().numpy() - ref).max() < 2e-2
+    assert_state_equal(be.quest, st)
+
+
+def test_determinism_bitwise():
+    q, _ = new_quest(2048, 64, 1, 4, 32768, 4, 128)
+    pool = rand_bf16((32768, 4, 128), seed=31).to(DEV)
+    for r in range(4):
+        q.update_prefill_representations(0, r, pool, torch.arange(32768 - 1000 * r, device=DEV))
+    queries = rand_bf16((4, 32, 128), seed=32).to(DEV)
+    seq = torch.tensor([32768, 31000, 30000, 29001], device=DEV)
+    q.prepare_step(seq)
+    a, _ = q.retrieve_topk(queries, 0, torch.arange(4, device=DEV), seq)
+    a = a.clone()
+    b, _ = q.retrieve_topk(queries, 0, torch.arange(4, device=DEV), seq)
+    assert torch.equal(a, b)
