@@ -5,11 +5,20 @@
 // hot-buffer rows (quest_hisparse.py:294-300).  Rows are attended exactly as
 // listed (a duplicate counts twice); scores, softmax and PV accumulate in fp32.
 //
-// Grid (chunks, bs): block (c, b) takes rows [c*64, c*64 + 64) of request b,
-// gathers them through the row map, computes per q head the chunk max m,
-// sum l = sum exp(s - m) and o = sum exp(s - m) v, and writes (m, l, o) to the
-// workspace.  The last chunk block of a request to finish (agent-scope ticket)
-// merges the partials: out = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c.
+// Two launches per call:
+//   1. chunk kernel, grid (chunks, bs): block (c, b) takes rows [64c, 64c + 64)
+//      of request b, gathers them through the row map and writes per q head the
+//      chunk max m, l = sum exp(s - m) and o = sum exp(s - m) v to the workspace.
+//      bf16 / head_dim 128 / group <= 16 uses MFMA (one wave per KV head):
+//        S^T = K Q^T with v_mfma_f32_16x16x32_bf16 - K rows are the A operand,
+//        16 bytes per lane straight from HBM, Q^T the B operand (query heads on
+//        N, padded to 16); the S^T accumulator gives each lane one head and 4
+//        consecutive tokens, which is exactly the A-operand layout of
+//        v_mfma_f32_16x16x16bf16_1k, so P = exp(S - m) (bf16) feeds O = P V
+//        without an LDS round trip; V comes in 8-byte row pieces (4 channels)
+//        transposed 4x4 in registers, channel d = 64*half + 4*lane + e.
+//      Other shapes / fp32 use a scalar kernel with the same partial format.
+//   2. merge kernel, grid (H, bs): out = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c.
 #include "qq_common.h"
 
 namespace qq {
@@ -60,7 +69,6 @@ __global__ __launch_bounds__(kThreads) void attn_chunk_kernel(AttnArgs a) {
   float* s_p = s_q + H * D;
   float* s_m = s_p + H * kChunk;
   float* s_l = s_m + H;
-  __shared__ int s_last;
 
   if (tid < cnt) {
     int64_t row;
@@ -118,30 +126,221 @@ __global__ __launch_bounds__(kThreads) void attn_chunk_kernel(AttnArgs a) {
     a.ws_ml[(part * H + h) * 2 + 1] = s_l[h];
   }
 
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-  __syncthreads();
-  if (tid == 0) s_last = (ticket_arrive(&a.tickets[b]) == nc - 1);
-  __syncthreads();
-  if (!s_last) return;
-  acquire_fence();
-  const int64_t base = (int64_t)b * a.max_chunks;
-  for (int idx = tid; idx < H * D; idx += kThreads) {
-    const int h = idx / D;
-    float M = -INFINITY;
-    for (int cc = 0; cc < nc; ++cc) M = fmaxf(M, a.ws_ml[((base + cc) * H + h) * 2]);
-    float L = 0.0f, O = 0.0f;
-    for (int cc = 0; cc < nc; ++cc) {
-      const float w = expf(a.ws_ml[((base + cc) * H + h) * 2] - M);
-      L += w * a.ws_ml[((base + cc) * H + h) * 2 + 1];
-      O += w * a.ws_o[(base + cc) * H * D + idx];
-    }
-    const float r = O / L;
-    if (a.q_dtype == QQ_DTYPE_BF16)
-      static_cast<uint16_t*>(a.out)[(int64_t)b * H * D + idx] = f2bf(r);
-    else
-      static_cast<float*>(a.out)[(int64_t)b * H * D + idx] = r;
+}
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef short short4_t __attribute__((ext_vector_type(4)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr int kMfmaDim = 128;
+
+__device__ inline int64_t chunk_row(const AttnArgs& a, int b, int i) {
+  int64_t row;
+  if (a.rows) {
+    row = a.rows[(int64_t)b * a.pos_stride + i];
+  } else {
+    const int64_t p = a.positions[(int64_t)b * a.pos_stride + i];
+    const int64_t req = a.rpi[b];
+    const bool ok = p >= 0 && p < a.r2t_stride && req >= 0 && req < a.r2t_rows;
+    row = ok ? (int64_t)a.r2t[req * a.r2t_stride + p] : 0;
   }
-  if (tid == 0) a.tickets[b] = 0;
+  return (row >= 0 && row < a.kv_rows) ? row : 0;
+}
+
+// bf16, head_dim 128, G = H/KV <= 16: one wave per KV head, 64 rows per block.
+template <int KV>
+__global__ __launch_bounds__(64 * KV) void attn_mfma_kernel(AttnArgs a) {
+  const int c = blockIdx.x, b = blockIdx.y;
+  const int n = (int)min((int64_t)a.actual[b], a.pos_stride);
+  const int nc = (n + kChunk - 1) / kChunk;
+  if (c >= nc) return;
+  const int r0 = c * kChunk, cnt = min(kChunk, n - r0);
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+  const int lo = l & 15, hi = l >> 4;
+  const int G = a.H / KV;
+  constexpr int kRow = KV * kMfmaDim;  // elements per pool row
+  __shared__ int64_t s_rows[kChunk];
+  if (threadIdx.x < kChunk) s_rows[threadIdx.x] = threadIdx.x < cnt ? chunk_row(a, b, r0 + threadIdx.x) : 0;
+  __syncthreads();
+
+  // K as the A operand: tile t (16 tokens) x k-step ks (32 channels): 16 bytes per lane.
+  const uint16_t* kbase = static_cast<const uint16_t*>(a.k) + w * kMfmaDim + hi * 8;
+  bf16x8_t ka[4][4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const uint16_t* kp = kbase + s_rows[t * 16 + lo] * kRow;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) ka[t][ks] = *reinterpret_cast<const bf16x8_t*>(kp + ks * 32);
+  }
+  // V row pieces for P V: k-step s (16 tokens), half hf, token j of the lane's 4.
+  const uint16_t* vbase = static_cast<const uint16_t*>(a.v) + w * kMfmaDim + lo * 4;
+  uint2 vr[4][2][4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint16_t* vp = vbase + s_rows[s * 16 + hi * 4 + j] * kRow;
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) vr[s][hf][j] = *reinterpret_cast<const uint2*>(vp + hf * 64);
+    }
+  // Q^T as the B operand: query head w*G + lo (zero past G), channels 8*hi + 32*ks.
+  bf16x8_t qb[4];
+  {
+    const uint16_t* qp = static_cast<const uint16_t*>(a.q) + (int64_t)b * a.q_bstride +
+                         (int64_t)(w * G + lo) * kMfmaDim + hi * 8;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      if (lo < G) {
+        qb[ks] = *reinterpret_cast<const bf16x8_t*>(qp + ks * 32);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qb[ks][e] = (__bf16)0.0f;
+      }
+    }
+  }
+
+  // S^T[token t*16 + 4*hi + i][head lo] in acc[t][i]
+  float4_t acc[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    acc[t] = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+      acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[t][ks], qb[ks], acc[t], 0, 0, 0);
+  }
+  const float sl2 = a.scale * kLog2e;
+  float mx = -INFINITY;
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int tok = t * 16 + hi * 4 + i;
+      const float x = tok < cnt ? acc[t][i] * sl2 : -INFINITY;
+      acc[t][i] = x;
+      mx = fmaxf(mx, x);
+    }
+  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  float sum = 0.0f;
+  short4_t pa[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint16_t pb = f2bf(exp2f(acc[t][i] - mx));
+      sum += bf2f(pb);
+      pa[t][i] = (short)pb;
+    }
+  sum += __shfl_xor(sum, 16, 64);
+  sum += __shfl_xor(sum, 32, 64);
+
+  // O[head 4*hi + i][d = 64*hf + 4*lo + e] in o[hf][e][i]
+  float4_t o[2][4];
+#pragma unroll
+  for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[hf][e] = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      short4_t vb[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint2 u = vr[s][hf][j];
+        vb[0][j] = (short)(u.x & 0xFFFFu);
+        vb[1][j] = (short)(u.x >> 16);
+        vb[2][j] = (short)(u.y & 0xFFFFu);
+        vb[3][j] = (short)(u.y >> 16);
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        o[hf][e] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa[s], vb[e], o[hf][e], 0, 0, 0);
+    }
+
+  const int64_t part = (int64_t)b * a.max_chunks + c;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int head = hi * 4 + i;
+    if (head < G) {
+      float* dst = a.ws_o + (part * a.H + w * G + head) * kMfmaDim + lo * 4;
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf)
+        *reinterpret_cast<float4*>(dst + hf * 64) =
+            make_float4(o[hf][0][i], o[hf][1][i], o[hf][2][i], o[hf][3][i]);
+    }
+  }
+  if (hi == 0 && lo < G) {
+    float* ml = a.ws_ml + (part * a.H + w * G + lo) * 2;
+    ml[0] = mx * kLn2;
+    ml[1] = sum;
+  }
+}
+
+// Combines the chunk partials of one (head, request): grid (H, bs).  The chunk
+// weights e^(m_c - M) / L are formed once in LDS; each thread then sums its
+// channels over the chunks with independent loads.
+constexpr int kMaxChunks = 1024;
+
+__global__ __launch_bounds__(kThreads) void attn_merge_kernel(AttnArgs a) {
+  const int h = blockIdx.x, b = blockIdx.y;
+  const int n = (int)min((int64_t)a.actual[b], a.pos_stride);
+  const int nc = min((n + kChunk - 1) / kChunk, kMaxChunks);
+  const int64_t base = (int64_t)b * a.max_chunks;
+  const int H = a.H, D = a.D;
+  __shared__ float s_w[kMaxChunks];
+  __shared__ float s_red[kThreads / 64];
+  const int nthr = blockDim.x, nwaves = nthr >> 6;
+  // M = max_c m_c
+  float m = -INFINITY;
+  for (int cc = threadIdx.x; cc < nc; cc += nthr) {
+    const float mc = a.ws_ml[((base + cc) * H + h) * 2];
+    s_w[cc] = mc;
+    m = fmaxf(m, mc);
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+  if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  float M = s_red[0];
+  for (int i = 1; i < nwaves; ++i) M = fmaxf(M, s_red[i]);
+  __syncthreads();
+  // L = sum_c e^(m_c - M) l_c ; s_w[c] = e^(m_c - M)
+  float lsum = 0.0f;
+  for (int cc = threadIdx.x; cc < nc; cc += nthr) {
+    const float e = expf(s_w[cc] - M);
+    s_w[cc] = e;
+    lsum += e * a.ws_ml[((base + cc) * H + h) * 2 + 1];
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) lsum += __shfl_xor(lsum, off, 64);
+  if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = lsum;
+  __syncthreads();
+  float L = 0.0f;
+  for (int i = 0; i < nwaves; ++i) L += s_red[i];
+  const float inv = nc > 0 ? 1.0f / L : 0.0f;
+  const float* op = a.ws_o + (base * H + h) * D;
+  const int64_t cstride = (int64_t)H * D;
+  for (int d = threadIdx.x; d < D; d += nthr) {
+    float O = 0.0f;
+    int cc = 0;
+    for (; cc + 8 <= nc; cc += 8) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = op[(cc + u) * cstride + d];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) O += s_w[cc + u] * v[u];
+    }
+    for (; cc < nc; ++cc) O += s_w[cc] * op[cc * cstride + d];
+    const float r = O * inv;
+    const int64_t oi = ((int64_t)b * H + h) * D + d;
+    if (a.q_dtype == QQ_DTYPE_BF16)
+      static_cast<uint16_t*>(a.out)[oi] = f2bf(r);
+    else
+      static_cast<float*>(a.out)[oi] = r;
+  }
 }
 
 int launch_attention(AttnArgs& a, int kv_dtype, int bs, int64_t workspace_bytes, void* workspace,
@@ -150,16 +349,30 @@ int launch_attention(AttnArgs& a, int kv_dtype, int bs, int64_t workspace_bytes,
   QQ_REQUIRE(workspace && workspace_bytes >= need, "%s: workspace %lld bytes < %lld needed", what,
              (long long)workspace_bytes, (long long)need);
   a.max_chunks = ceil_div(a.pos_stride, kChunk);
+  QQ_REQUIRE(a.max_chunks <= kMaxChunks, "%s: %lld rows per request exceed %d", what,
+             (long long)a.pos_stride, kMaxChunks * kChunk);
   a.ws_o = static_cast<float*>(workspace);
   a.ws_ml = a.ws_o + (int64_t)bs * a.max_chunks * a.H * a.D;
   const size_t smem = kChunk * sizeof(int64_t) + (size_t)(a.H * a.D + a.H * kChunk + 2 * a.H) * 4;
   QQ_REQUIRE(smem <= 64 * 1024, "%s: %d heads x %d dims need too much LDS", what, a.H, a.D);
   dim3 grid(max(1, a.max_chunks), bs);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (kv_dtype == QQ_DTYPE_BF16)
+  const int G = a.H / a.KV;
+  const bool mfma = a.q_dtype == QQ_DTYPE_BF16 && kv_dtype == QQ_DTYPE_BF16 && a.D == kMfmaDim &&
+                    G <= 16 && (a.KV == 1 || a.KV == 2 || a.KV == 4 || a.KV == 8);
+  if (mfma) {
+    switch (a.KV) {
+      case 1: attn_mfma_kernel<1><<<grid, 64, 0, s>>>(a); break;
+      case 2: attn_mfma_kernel<2><<<grid, 128, 0, s>>>(a); break;
+      case 4: attn_mfma_kernel<4><<<grid, 256, 0, s>>>(a); break;
+      default: attn_mfma_kernel<8><<<grid, 512, 0, s>>>(a); break;
+    }
+  } else if (kv_dtype == QQ_DTYPE_BF16) {
     attn_chunk_kernel<uint16_t><<<grid, kThreads, smem, s>>>(a);
-  else
+  } else {
     attn_chunk_kernel<float><<<grid, kThreads, smem, s>>>(a);
+  }
+  attn_merge_kernel<<<dim3(a.H, bs), a.D <= 128 ? 128 : kThreads, 0, s>>>(a);
   return check_launch(what);
 }
 

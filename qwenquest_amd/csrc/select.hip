@@ -1,19 +1,21 @@
-// Quest page scoring + top-k page selection + token layout, one launch per layer.
+// Quest page scoring + top-k page selection + token layout.
 //
 // Reference: src/qwenquest/quest.py:366-464 (group_queries, page_scores,
 // retrieve_topk) and the layout of prepare_step (quest.py:333-342).
 //
-// Grid (blocks_per_request, bs).  Each block averages q over the GQA group,
-// then its 4 waves score pages: lane l holds channels [l*m, l*m + m) of the
-// page (m = ceil(KV*D / 64)), so a wave reads one page's KV*D (min, max) words
-// as one coalesced 2 KiB stream at KV*D = 512.  Per page the lane adds its m
-// fp32 products in channel order and the 64 lane sums are combined by a
-// halving tree (acc[l] += acc[l + w], w = 32 .. 1) - the canonical order the
-// oracle reproduces.  The last block of a request to finish (agent-scope
-// ticket) selects the top k = top_k/P - 1 pages with a 4-pass radix select on
-// order-preserving 32-bit keys, breaks ties at the threshold by lowest page
-// index, ranks the k winners by (score desc, page asc) and writes the
-// positions.  Short requests (seq <= top_k) only get the dense layout.
+// Launch 1, grid (page blocks, bs): each block averages q over the GQA group,
+// then its 4 waves score candidate pages [0, candidate_limit): lane l holds
+// channels [l*m, l*m + m) of the page (m = ceil(KV*D / 64)), so a wave reads a
+// page's KV*D (min, max) words as one coalesced 2 KiB stream at KV*D = 512.
+// Per page the lane adds its m fp32 products in channel order and the 64 lane
+// sums are combined by a halving tree (acc[l] += acc[l + w], w = 32 .. 1) - the
+// canonical order the oracle reproduces.
+// Launch 2, one block per request: the top k = top_k/P - 1 pages by (score desc,
+// page asc), then positions (pages x P, then the recent window); short requests
+// get the dense layout.  k <= 64 over <= 4096 pages: a threshold from the
+// per-thread maxima filters the keys, survivors are rank-counted; otherwise a 4-pass radix
+// select on order-preserving 32-bit keys with ties at the threshold to the
+// lowest page index.
 #include "qq_common.h"
 
 namespace qq {
@@ -85,12 +87,65 @@ __device__ inline float gqa_mean(const void* q, int dtype, int64_t qb, int G, in
   return dtype == QQ_DTYPE_BF16 ? bf2f(f2bf(acc)) : acc;
 }
 
-// Lane `lane` adds channels lane*m .. lane*m + m - 1 (m <= M, channels >= C count
-// as +0.0), then the 64 lane sums are combined by the halving tree.
+// Lane partials of 8 pages at once.  acc[p] is this lane's partial of page p
+// (its m channels, summed in order).  The 8 halving trees are interleaved: at
+// level w = 32, 16, 8 each lane keeps half of its pages and adds the partner's
+// (lane l ^ w) partial of them - the pairs are exactly the tree's (i, i + w) -
+// then levels 4, 2, 1 run on one value.  Lane l ends with page l >> 3.
+__device__ inline float reduce8_pages(float (&acc)[8], int lane) {
+  const bool up32 = lane & 32, up16 = lane & 16, up8 = lane & 8;
+  float v4[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float send = up32 ? acc[j] : acc[4 + j];
+    const float keep = up32 ? acc[4 + j] : acc[j];
+    v4[j] = __fadd_rn(keep, __shfl_xor(send, 32, 64));
+  }
+  float v2[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const float send = up16 ? v4[j] : v4[2 + j];
+    const float keep = up16 ? v4[2 + j] : v4[j];
+    v2[j] = __fadd_rn(keep, __shfl_xor(send, 16, 64));
+  }
+  float v;
+  {
+    const float send = up8 ? v2[0] : v2[1];
+    const float keep = up8 ? v2[1] : v2[0];
+    v = __fadd_rn(keep, __shfl_xor(send, 8, 64));
+  }
+  v = __fadd_rn(v, __shfl_xor(v, 4, 64));
+  v = __fadd_rn(v, __shfl_xor(v, 2, 64));
+  v = __fadd_rn(v, __shfl_xor(v, 1, 64));
+  return v;
+}
+
+// This lane's m channels of one page, products summed in channel order.
 template <int M>
-__device__ inline float score_page(const uint32_t* pb, const float* qreg, int lane, int m, int C) {
-  uint32_t w[M];
-  if (M % 4 == 0 && m == M && C == 64 * M) {
+__device__ inline float lane_partial(const uint32_t (&w)[M], const float (&qreg)[M], int lane, int m,
+                                     int C) {
+  float acc = 0.0f;
+#pragma unroll
+  for (int j = 0; j < M; ++j) {
+    const int c = lane * m + j;
+    const float qv = qreg[j];
+    const float kv = qv >= 0.0f ? bf2f((uint16_t)(w[j] >> 16)) : bf2f((uint16_t)(w[j] & 0xFFFFu));
+    const float prod = (j < m && c < C) ? __fmul_rn(qv, kv) : 0.0f;
+    if (j == 0)
+      acc = prod;
+    else if (j < m)
+      acc = __fadd_rn(acc, prod);
+  }
+  return acc;
+}
+
+template <int M>
+__device__ inline void load_lane_words(uint32_t (&w)[M], const uint32_t* pb, int lane, int m, int C,
+                                       bool valid) {
+  if (!valid) {
+#pragma unroll
+    for (int j = 0; j < M; ++j) w[j] = 0u;
+  } else if (M % 4 == 0 && m == M && C == 64 * M) {
     const uint4* p4 = reinterpret_cast<const uint4*>(pb + lane * M);
 #pragma unroll
     for (int i = 0; i < M / 4; ++i) {
@@ -107,83 +162,91 @@ __device__ inline float score_page(const uint32_t* pb, const float* qreg, int la
       w[j] = (j < m && c < C) ? pb[c] : 0u;
     }
   }
-  float acc = 0.0f;
+}
+
+// q-bar of this lane's channels c = lane*m + j, in registers (no LDS, no barrier).
+template <int M>
+__device__ inline void lane_qbar(float (&qreg)[M], const void* q, int dtype, int64_t qb, int G,
+                                 int D, int m, int C, int lane) {
+  if (dtype == QQ_DTYPE_BF16 && M == 8 && m == 8 && D % 8 == 0 && G > 1) {
+    const int c0 = lane * 8;
+    if (c0 >= C) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) qreg[j] = 0.0f;
+      return;
+    }
+    const int h = c0 / D, d0 = c0 - h * D;
+    float acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
+    const uint16_t* qp = static_cast<const uint16_t*>(q) + qb + (int64_t)h * G * D + d0;
+    for (int g = 0; g < G; ++g) {
+      const uint4 u = *reinterpret_cast<const uint4*>(qp + (int64_t)g * D);
+      const uint32_t wv[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        acc[2 * j] = __fadd_rn(acc[2 * j], bf2f((uint16_t)(wv[j] & 0xFFFFu)));
+        acc[2 * j + 1] = __fadd_rn(acc[2 * j + 1], bf2f((uint16_t)(wv[j] >> 16)));
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) qreg[j] = bf2f(f2bf(acc[j] / (float)G));
+    return;
+  }
 #pragma unroll
   for (int j = 0; j < M; ++j) {
     const int c = lane * m + j;
-    const float qv = qreg[j];
-    const float kv = qv >= 0.0f ? bf2f((uint16_t)(w[j] >> 16)) : bf2f((uint16_t)(w[j] & 0xFFFFu));
-    const float prod = (j < m && c < C) ? __fmul_rn(qv, kv) : 0.0f;
-    if (j == 0)
-      acc = prod;
-    else if (j < m)
-      acc = __fadd_rn(acc, prod);
+    qreg[j] = (j < m && c < C) ? gqa_mean(q, dtype, qb, G, D, c) : 0.0f;
   }
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) acc = __fadd_rn(acc, __shfl_down(acc, off, 64));
-  return acc;
 }
 
 template <int M>
-__global__ __launch_bounds__(kThreads) void score_select_kernel(SelectArgs a) {
+__global__ __launch_bounds__(kThreads) void score_candidates_kernel(SelectArgs a) {
   const int b = blockIdx.y;
+  const int64_t s = a.seq[b];
+  if (s <= a.top_k || a.k_sel == 0) return;  // dense layout / recent window only
+  const int lim = min(a.limit[b], a.MP);
+  const int p0 = blockIdx.x * a.ppb;
+  if (p0 >= lim) return;
+  const int64_t req = a.rpi[b];
+  if (req < 0 || req >= a.R) return;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int pw = p0 + wave * 8;  // this wave's 8 pages
+  if (pw >= lim) return;
+  const uint32_t* pbase = a.bounds_layer + req * a.MP * a.C;
+  uint32_t w[8][M];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    load_lane_words<M>(w[i], pbase + (int64_t)(pw + i) * a.C, lane, a.m, a.C, pw + i < lim);
+  float qreg[M];
+  lane_qbar<M>(qreg, a.q, a.q_dtype, (int64_t)b * a.q_bstride, a.H / a.KV, a.D, a.m, a.C, lane);
+  float acc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc[i] = lane_partial<M>(w[i], qreg, lane, a.m, a.C);
+  const float v = reduce8_pages(acc, lane);
+  const int p = pw + (lane >> 3);
+  if ((lane & 7) == 0 && p < lim) a.scores[(int64_t)b * a.MP + p] = v;
+}
+
+// One block per request: top k_sel pages (quest.py:450-452) + token layout (453-460).
+__global__ __launch_bounds__(kThreads) void select_layout_kernel(SelectArgs a) {
+  const int b = blockIdx.x;
   const int tid = threadIdx.x;
   const int64_t s = a.seq[b];
   int32_t* pos = a.positions + (int64_t)b * a.top_k;
-
   if (s <= a.top_k) {  // dense layout, quest.py:339-342 / 460
-    if (blockIdx.x == 0)
-      for (int j = tid; j < a.top_k; j += kThreads)
-        pos[j] = (int32_t)min((int64_t)j, max(s - 1, (int64_t)0));
+    for (int j = tid; j < a.top_k; j += kThreads) pos[j] = (int32_t)min((int64_t)j, max(s - 1, (int64_t)0));
     return;
   }
   const int k = a.k_sel;
   if (k == 0) {  // top_k == P: the recent window is the whole layout (quest.py:457-458)
-    if (blockIdx.x == 0) write_recent(pos, s, a.P);
+    write_recent(pos, s, a.P);
     return;
   }
-  const int lim = min(a.limit[b], a.MP);
-  const int n_eff = max(lim, k);
-  const int nblk = max(1, (lim + a.ppb - 1) / a.ppb);
-  if ((int)blockIdx.x >= nblk) return;
-
-  __shared__ float s_q[kMaxC];
-  __shared__ int s_last;
-  for (int c = tid; c < a.C; c += kThreads)
-    s_q[c] = gqa_mean(a.q, a.q_dtype, (int64_t)b * a.q_bstride, a.H / a.KV, a.D, c);
-  __syncthreads();
-
-  const int wave = tid >> 6, lane = tid & 63;
-  float qreg[M];
-#pragma unroll
-  for (int j = 0; j < M; ++j) {
-    const int c = lane * a.m + j;
-    qreg[j] = (j < a.m && c < a.C) ? s_q[c] : 0.0f;
-  }
   const int64_t req = a.rpi[b];
-  const bool req_ok = req >= 0 && req < a.R;
-  const uint32_t* pbase = a.bounds_layer + (req_ok ? req : 0) * a.MP * a.C;
-  float* sc = a.scores + (int64_t)b * a.MP;
-  const int p0 = blockIdx.x * a.ppb;
-  const int p1 = req_ok ? min(p0 + a.ppb, lim) : p0;
-  for (int p = p0 + wave; p < p1; p += 2 * kWaves) {
-    const int p2 = p + kWaves;
-    const float s0 = score_page<M>(pbase + (int64_t)p * a.C, qreg, lane, a.m, a.C);
-    float s1 = 0.0f;
-    if (p2 < p1) s1 = score_page<M>(pbase + (int64_t)p2 * a.C, qreg, lane, a.m, a.C);
-    if (lane == 0) {
-      sc[p] = s0;
-      if (p2 < p1) sc[p2] = s1;
-    }
-  }
-
-  // ---- last block of this request selects (quest.py:450-460)
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-  __syncthreads();
-  if (tid == 0) s_last = (ticket_arrive(&a.tickets[b]) == nblk - 1);
-  __syncthreads();
-  if (!s_last) return;
-  acquire_fence();
+  const int lim = (req >= 0 && req < a.R) ? min(a.limit[b], a.MP) : 0;
+  const int n_eff = max(lim, k);
+  const float* sc = a.scores + (int64_t)b * a.MP;
 
   __shared__ uint32_t s_hist[256];
   __shared__ uint32_t s_prefix, s_mask;
@@ -270,7 +333,97 @@ __global__ __launch_bounds__(kThreads) void score_select_kernel(SelectArgs a) {
     pos[slot] = s_order[r] * P + (slot - r * P);
   }
   write_recent(pos + (int64_t)k * P, s, P);
-  if (tid == 0) a.tickets[b] = 0;
+}
+
+// 64-bit selection key: order-preserving score in the high word, ~page in the
+// low word, so "larger key" = higher score, then lower page index.
+__device__ inline uint64_t sel_key(uint32_t score_key, int page) {
+  return ((uint64_t)score_key << 32) | (uint32_t)(~(uint32_t)page);
+}
+
+// Top k <= 64 pages of n_eff <= 256*KPT keys, one block per request, no atomics
+// on hot bins and no long dependent shuffle chains:
+//   1. each thread holds KPT keys (pages tid + 256 i) and their max;
+//   2. T0 = the k-th largest of the 256 thread maxima (LDS rank counting).  The
+//      k largest maxima are k distinct keys >= T0, so the true k-th largest key
+//      is >= T0 and every top-k key survives the filter key >= T0;
+//   3. survivors are compacted into LDS (ballot + mbcnt per wave);
+//   4. each survivor's rank = number of survivors above it; ranks < k give the
+//      pages in (score desc, page asc) order.
+template <int KPT>
+__global__ __launch_bounds__(kThreads) void select_filter_kernel(SelectArgs a) {
+  const int b = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int64_t s = a.seq[b];
+  int32_t* pos = a.positions + (int64_t)b * a.top_k;
+  if (s <= a.top_k) {
+    for (int j = tid; j < a.top_k; j += kThreads) pos[j] = (int32_t)min((int64_t)j, max(s - 1, (int64_t)0));
+    return;
+  }
+  const int k = a.k_sel;
+  if (k == 0) {
+    write_recent(pos, s, a.P);
+    return;
+  }
+  const int64_t req = a.rpi[b];
+  const int lim = (req >= 0 && req < a.R) ? min(a.limit[b], a.MP) : 0;
+  const int n_eff = max(lim, k);
+  const float* sc = a.scores + (int64_t)b * a.MP;
+  constexpr uint32_t kNegInfKey = 0x007FFFFFu;  // orderable(-inf): masked pages (quest.py:451)
+
+  uint64_t key[KPT];
+  uint64_t tmax = 0ull;
+#pragma unroll
+  for (int i = 0; i < KPT; ++i) {
+    const int p = tid + kThreads * i;
+    key[i] = p < n_eff ? sel_key(p < lim ? orderable(sc[p]) : kNegInfKey, p) : 0ull;
+    tmax = key[i] > tmax ? key[i] : tmax;
+  }
+  __shared__ uint64_t s_max[kThreads];
+  __shared__ uint64_t s_cand[kThreads * KPT];
+  __shared__ uint64_t s_t0;
+  __shared__ int s_nz, s_nc;
+  __shared__ int s_order[64];
+  if (tid == 0) {
+    s_t0 = 0ull;
+    s_nz = 0;
+    s_nc = 0;
+  }
+  s_max[tid] = tmax;
+  __syncthreads();
+  if (tmax != 0ull) atomicAdd(&s_nz, 1);
+  int rank = 0;
+  for (int j = 0; j < kThreads; ++j) rank += s_max[j] > tmax;
+  __syncthreads();
+  if (s_nz >= k && tmax != 0ull && rank == k - 1) s_t0 = tmax;  // unique: nonzero keys differ
+  __syncthreads();
+  const uint64_t t0 = s_t0;
+  const int lane = tid & 63;
+#pragma unroll
+  for (int i = 0; i < KPT; ++i) {
+    const bool take = key[i] != 0ull && key[i] >= t0;
+    const uint64_t mask = __ballot(take);
+    int base = 0;
+    if (lane == 0 && mask) base = atomicAdd(&s_nc, __popcll(mask));
+    base = __shfl(base, 0, 64);
+    if (take) s_cand[base + __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
+                                                      __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u))] = key[i];
+  }
+  __syncthreads();
+  const int nc = s_nc;
+  for (int i = tid; i < nc; i += kThreads) {
+    const uint64_t ci = s_cand[i];
+    int r = 0;
+    for (int j = 0; j < nc; ++j) r += s_cand[j] > ci;
+    if (r < k) s_order[r] = (int)(~(uint32_t)ci);
+  }
+  __syncthreads();
+  const int P = a.P;
+  for (int slot = tid; slot < k * P; slot += kThreads) {
+    const int r = slot / P;
+    pos[slot] = s_order[r] * P + (slot - r * P);
+  }
+  write_recent(pos + (int64_t)k * P, s, P);
 }
 
 // group_queries (quest.py:366-391) as its own kernel: out [bs, C] in q's dtype.
@@ -296,21 +449,26 @@ __global__ __launch_bounds__(kThreads) void page_scores_kernel(const void* qbar,
                                                              int C, int m, float* scores) {
   const int b = blockIdx.y;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t req = rpi[b];
+  if (req < 0 || req >= R) return;
+  const int pw = blockIdx.x * kPagesPerBlock + wave * 8;
+  if (pw >= MP) return;
   float qreg[M];
 #pragma unroll
   for (int j = 0; j < M; ++j) {
     const int c = lane * m + j;
     qreg[j] = (j < m && c < C) ? load_as_float(qbar, (int64_t)b * bstride + c, dtype) : 0.0f;
   }
-  const int64_t req = rpi[b];
-  if (req < 0 || req >= R) return;
   const uint32_t* pbase = bounds_layer + req * (int64_t)MP * C;
-  const int p0 = blockIdx.x * kPagesPerBlock;
-  const int p1 = min(p0 + kPagesPerBlock, MP);
-  for (int p = p0 + wave; p < p1; p += kWaves) {
-    const float sc = score_page<M>(pbase + (int64_t)p * C, qreg, lane, m, C);
-    if (lane == 0) scores[(int64_t)b * MP + p] = sc;
-  }
+  uint32_t w[8][M];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) load_lane_words<M>(w[i], pbase + (int64_t)(pw + i) * C, lane, m, C, pw + i < MP);
+  float acc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc[i] = lane_partial<M>(w[i], qreg, lane, m, C);
+  const float v = reduce8_pages(acc, lane);
+  const int p = pw + (lane >> 3);
+  if ((lane & 7) == 0 && p < MP) scores[(int64_t)b * MP + p] = v;
 }
 
 }  // namespace
@@ -412,14 +570,21 @@ extern "C" int qq_quest_retrieve_topk(const void* q, int q_dtype, int64_t q_batc
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int M = (C + 63) / 64;
   if (M <= 1)
-    score_select_kernel<1><<<grid, kThreads, 0, s>>>(a);
+    score_candidates_kernel<1><<<grid, kThreads, 0, s>>>(a);
   else if (M <= 2)
-    score_select_kernel<2><<<grid, kThreads, 0, s>>>(a);
+    score_candidates_kernel<2><<<grid, kThreads, 0, s>>>(a);
   else if (M <= 4)
-    score_select_kernel<4><<<grid, kThreads, 0, s>>>(a);
+    score_candidates_kernel<4><<<grid, kThreads, 0, s>>>(a);
   else if (M <= 8)
-    score_select_kernel<8><<<grid, kThreads, 0, s>>>(a);
+    score_candidates_kernel<8><<<grid, kThreads, 0, s>>>(a);
   else
-    score_select_kernel<16><<<grid, kThreads, 0, s>>>(a);
+    score_candidates_kernel<16><<<grid, kThreads, 0, s>>>(a);
+  const int n_max = max(max_pages, k_sel);
+  if (k_sel <= 64 && n_max <= 8 * kThreads)
+    select_filter_kernel<8><<<bs, kThreads, 0, s>>>(a);
+  else if (k_sel <= 64 && n_max <= 16 * kThreads)
+    select_filter_kernel<16><<<bs, kThreads, 0, s>>>(a);
+  else
+    select_layout_kernel<<<bs, kThreads, 0, s>>>(a);
   return check_launch("qq_quest_retrieve_topk");
 }
