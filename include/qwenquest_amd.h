@@ -109,14 +109,12 @@ int qq_quest_prepare_step(const int64_t* seq_lens, int bs, int page_size, int to
  * requests: the top_k/P - 1 best complete pages by descending score, ties to
  * the lowest page index, expanded x P, then the recent window; short
  * requests: 0..seq-1 padded with seq-1).  Page scores of candidate pages are
- * left in scores_ws [bs, max_pages] fp32.  `tickets` [bs] int32 must be zero
- * on entry and is zero again on exit. */
+ * left in scores_ws [bs, max_pages] fp32. */
 int qq_quest_retrieve_topk(const void* q, int q_dtype, int64_t q_batch_stride, int num_q_heads,
                            const uint16_t* page_k_bounds, int layer, const int64_t* req_pool_indices,
                            const int64_t* seq_lens, const int32_t* candidate_limit, int bs,
                            int max_reqs, int max_pages, int kv_heads, int head_dim, int page_size,
-                           int top_k, float* scores_ws, int32_t* tickets, int32_t* positions,
-                           void* stream);
+                           int top_k, float* scores_ws, int32_t* positions, void* stream);
 
 /* Replaces QuestAlgorithm.group_queries (src/qwenquest/quest.py:366-391):
  * out[b, h, d] = mean over the G = num_q_heads / kv_heads query heads of KV
@@ -145,8 +143,7 @@ int64_t qq_decode_attention_workspace_bytes(int bs, int max_rows, int num_q_head
  * (duplicates counted), softmax(q.k * scale) in fp32, output [bs, H*D] in
  * q's dtype.  k_layer/v_layer: this layer's [kv_rows, KV, D] pool;
  * req_to_token: [req_to_token_rows, req_to_token_stride] int32.  Out-of-range
- * requests, positions or rows read the padding row 0 instead of faulting.
- * `tickets` [bs] int32 zero on entry and exit. */
+ * requests, positions or rows read the padding row 0 instead of faulting. */
 int qq_quest_decode_attention(const void* q, int q_dtype, int64_t q_batch_stride,
                               int num_q_heads, const void* k_layer, const void* v_layer,
                               int kv_dtype, int64_t kv_rows, int kv_heads, int head_dim,
@@ -155,7 +152,7 @@ int qq_quest_decode_attention(const void* q, int q_dtype, int64_t q_batch_stride
                               const int32_t* positions,
                               int64_t positions_stride, const int32_t* actual_lens, int bs,
                               float scale, void* out, void* workspace, int64_t workspace_bytes,
-                              int32_t* tickets, void* stream);
+                              void* stream);
 
 /* Replaces the Mode-3 attention of QuestHiSparseBackend.forward_decode
  * (src/qwenquest/attention/quest_hisparse.py:294-300): like
@@ -165,8 +162,27 @@ int qq_decode_attention_rows(const void* q, int q_dtype, int64_t q_batch_stride,
                              const void* k_layer, const void* v_layer, int kv_dtype,
                              int64_t kv_rows, int kv_heads, int head_dim, const int64_t* rows,
                              int64_t rows_stride, const int32_t* actual_lens, int bs, float scale,
-                             void* out, void* workspace, int64_t workspace_bytes,
-                             int32_t* tickets, void* stream);
+                             void* out, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Replaces QuestOnlyBackend.forward_decode (src/qwenquest/attention/quest_only.py:132-159)
+ * for one layer in four launches: the new tokens' K/V (k_new/v_new [bs, KV, D])
+ * go to rows out_cache_loc of k_layer/v_layer (memory.py:114-120; skipped when
+ * k_new is NULL), then retrieve_topk (quest.py:409-464) writes positions
+ * [bs, top_k], then attention over req_to_token[req, positions[:n]] writes out
+ * [bs, H*D] (ops.py:48-66).  seq_lens / candidate_limit / actual_lens are the
+ * step's prepare_step outputs; workspace sized by
+ * qq_decode_attention_workspace_bytes(bs, top_k, H, D). */
+int qq_quest_forward_decode(const void* q, int q_dtype, int64_t q_batch_stride, int num_q_heads,
+                            const void* k_new, const void* v_new, int new_dtype,
+                            const int64_t* out_cache_loc, void* k_layer, void* v_layer,
+                            int kv_dtype, int64_t kv_rows, const uint16_t* page_k_bounds,
+                            int layer, const int64_t* req_pool_indices, const int64_t* seq_lens,
+                            const int32_t* candidate_limit, const int32_t* actual_lens, int bs,
+                            int max_reqs, int max_pages, int kv_heads, int head_dim,
+                            int page_size, int top_k, const int32_t* req_to_token,
+                            int64_t req_to_token_stride, int64_t req_to_token_rows, float scale,
+                            float* scores_ws, int32_t* positions, void* out, void* workspace,
+                            int64_t workspace_bytes, void* stream);
 
 /* Replaces MHATokenToKVPool.set_kv_buffer (src/qwenquest/memory.py:114-120):
  * k_layer[locs[i]] = k[i], v_layer[locs[i]] = v[i] (row = KV*D elements),

@@ -41,18 +41,23 @@ SIGNATURES: dict[str, tuple] = {
     "qq_quest_prepare_step": (_I, [_P, _I, _I, _I, _I, _P, _P, _P]),
     "qq_quest_retrieve_topk": (
         _I,
-        [_P, _I, _L, _I, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P],
+        [_P, _I, _L, _I, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P],
     ),
     "qq_quest_group_queries": (_I, [_P, _I, _L, _I, _I, _I, _I, _P, _P]),
     "qq_quest_page_scores": (_I, [_P, _I, _L, _P, _I, _P, _I, _I, _I, _I, _I, _P, _P]),
     "qq_decode_attention_workspace_bytes": (_L, [_I, _I, _I, _I]),
     "qq_quest_decode_attention": (
         _I,
-        [_P, _I, _L, _I, _P, _P, _I, _L, _I, _I, _P, _L, _L, _P, _P, _L, _P, _I, _F, _P, _P, _L, _P, _P],
+        [_P, _I, _L, _I, _P, _P, _I, _L, _I, _I, _P, _L, _L, _P, _P, _L, _P, _I, _F, _P, _P, _L, _P],
     ),
     "qq_decode_attention_rows": (
         _I,
-        [_P, _I, _L, _I, _P, _P, _I, _L, _I, _I, _P, _L, _P, _I, _F, _P, _P, _L, _P, _P],
+        [_P, _I, _L, _I, _P, _P, _I, _L, _I, _I, _P, _L, _P, _I, _F, _P, _P, _L, _P],
+    ),
+    "qq_quest_forward_decode": (
+        _I,
+        [_P, _I, _L, _I, _P, _P, _I, _P, _P, _P, _I, _L, _P, _I, _P, _P, _P, _P, _I, _I, _I, _I,
+         _I, _I, _I, _P, _L, _L, _F, _P, _P, _P, _P, _L, _P],
     ),
     "qq_kv_scatter": (_I, [_P, _P, _I, _L, _P, _P, _I, _P, _I, _L, _P]),
 }

@@ -16,20 +16,17 @@ __all__ = ["decode_attention", "extend_attention", "AttentionWorkspace"]
 
 
 class AttentionWorkspace:
-    """Device workspace + per-request tickets for the split-K attention kernels."""
+    """Device workspace of the split-K attention kernels (per-chunk (m, l, o) partials)."""
 
     def __init__(self, device: torch.device):
         self.device = device
         self.buf = torch.empty(0, dtype=torch.uint8, device=device)
-        self.tickets = torch.zeros(0, dtype=torch.int32, device=device)
 
-    def get(self, bs: int, max_rows: int, heads: int, head_dim: int) -> tuple[torch.Tensor, torch.Tensor]:
+    def get(self, bs: int, max_rows: int, heads: int, head_dim: int) -> torch.Tensor:
         need = int(_lib.load().qq_decode_attention_workspace_bytes(bs, max_rows, heads, head_dim))
         if self.buf.numel() < need:
             self.buf = torch.empty(need, dtype=torch.uint8, device=self.device)
-        if self.tickets.numel() < bs:
-            self.tickets = torch.zeros(bs, dtype=torch.int32, device=self.device)
-        return self.buf, self.tickets
+        return self.buf
 
 
 _workspaces: dict[torch.device, AttentionWorkspace] = {}
@@ -64,13 +61,13 @@ def decode_attention_rows(
     rows = rows.to(torch.int64).contiguous()
     actual = actual_lens.to(device=q.device, dtype=torch.int32).contiguous()
     ws = workspace or _workspace(q.device)
-    buf, tickets = ws.get(bs, rows.shape[1], heads, dim)
+    buf = ws.get(bs, rows.shape[1], heads, dim)
     res = out if out is not None else torch.empty((bs, heads * dim), dtype=q.dtype, device=q.device)
     _lib.call(
         "qq_decode_attention_rows", _lib.ptr(q), _lib.dtype_code(q.dtype), q.stride(0), heads,
         _lib.ptr(k_buf), _lib.ptr(v_buf), _lib.dtype_code(k_buf.dtype), k_buf.shape[0], kv, dim,
         _lib.ptr(rows), rows.stride(0), _lib.ptr(actual), bs, float(scaling), _lib.ptr(res),
-        _lib.ptr(buf), buf.numel(), _lib.ptr(tickets), _lib.stream(q.device),
+        _lib.ptr(buf), buf.numel(), _lib.stream(q.device),
     )
     return res
 

@@ -106,14 +106,46 @@ class QuestOnlyBackend(AttentionBackend):
     # ------------------------------------------------------------------ decode
 
     def forward_decode(self, q, k, v, layer, batch: ForwardBatch) -> torch.Tensor:
-        """quest_only.py:132-159: save K/V, select, then gather + attend in one kernel."""
+        """quest_only.py:132-159 in one C call: save the new K/V, select, gather + attend."""
         assert batch.out_cache_loc is not None
-        self.token_to_kv_pool.set_kv_buffer(layer.layer_id, batch.out_cache_loc, k, v)
+        quest = self.quest
+        step = quest._step
+        if step is None:
+            raise RuntimeError("prepare_step() must be called once per decode step first")
+        pool = self.token_to_kv_pool
         bs = batch.batch_size
-        positions, actual = self.quest.retrieve_topk(
-            q, layer.layer_id, batch.req_pool_indices, batch.seq_lens, out=self._positions
+        q3 = quest._queries_3d(q)
+        heads, dim = q3.shape[1], pool.head_dim
+        if step.seq_lens.shape[0] != bs:
+            raise ValueError("batch size differs from the one given to prepare_step()")
+        kn = k.reshape(bs, pool.kv_heads * dim)
+        vn = v.reshape(bs, pool.kv_heads * dim)
+        if kn.dtype != vn.dtype or kn.dtype not in (torch.bfloat16, torch.float32):
+            kn, vn = kn.to(pool.dtype), vn.to(pool.dtype)
+        kn, vn = kn.contiguous(), vn.contiguous()
+        loc = batch.out_cache_loc
+        if loc.dtype != torch.int64 or not loc.is_contiguous():
+            loc = loc.to(torch.int64).contiguous()
+        rpi = batch.req_pool_indices
+        if rpi.dtype != torch.int64 or not rpi.is_contiguous():
+            rpi = rpi.to(torch.int64).contiguous()
+        k_buf, v_buf = pool.get_kv_buffer(layer.layer_id)
+        buf = self._attn_ws.get(bs, quest.top_k, heads, dim)
+        out = torch.empty((bs, heads * dim), dtype=q3.dtype, device=q3.device)
+        r2t = self.req_to_token
+        _lib.call(
+            "qq_quest_forward_decode", _lib.ptr(q3), _lib.dtype_code(q3.dtype), q3.stride(0), heads,
+            _lib.ptr(kn), _lib.ptr(vn), _lib.dtype_code(kn.dtype), _lib.ptr(loc), _lib.ptr(k_buf),
+            _lib.ptr(v_buf), _lib.dtype_code(k_buf.dtype), k_buf.shape[0], _lib.ptr(quest.page_k_bounds),
+            layer.layer_id - quest.start_layer, _lib.ptr(rpi), _lib.ptr(step.seq_lens),
+            _lib.ptr(step.candidate_limit_i32), _lib.ptr(step.actual_lens), bs, quest.max_reqs,
+            quest.max_pages_per_req, quest.kv_heads, quest.head_dim, quest.page_size, quest.top_k,
+            _lib.ptr(r2t), r2t.stride(0), r2t.shape[0], float(layer.scaling), _lib.ptr(quest._scores_ws),
+            _lib.ptr(self._positions), _lib.ptr(out), _lib.ptr(buf), buf.numel(), _lib.stream(q3.device),
         )
-        return self.sparse_attention(q, layer, batch.req_pool_indices, positions, actual, bs)
+        if quest.trace is not None:
+            quest._record(layer.layer_id, rpi, step, self._positions[:bs])
+        return out
 
     def sparse_attention(self, q, layer, req_pool_indices, positions, actual, bs) -> torch.Tensor:
         """[Q7] rows = req_to_token[req, positions[:n]] -> attention over exactly those rows."""
@@ -125,7 +157,7 @@ class QuestOnlyBackend(AttentionBackend):
         if rpi.dtype != torch.int64 or rpi.device != q3.device:
             rpi = rpi.to(device=q3.device, dtype=torch.int64)
         rpi = rpi.contiguous()
-        buf, tickets = self._attn_ws.get(bs, positions.shape[1], heads, dim)
+        buf = self._attn_ws.get(bs, positions.shape[1], heads, dim)
         out = torch.empty((bs, heads * dim), dtype=q3.dtype, device=q3.device)
         r2t = self.req_to_token
         _lib.call(
@@ -133,7 +165,7 @@ class QuestOnlyBackend(AttentionBackend):
             _lib.ptr(k_buf), _lib.ptr(v_buf), _lib.dtype_code(k_buf.dtype), k_buf.shape[0],
             self.token_to_kv_pool.kv_heads, dim, _lib.ptr(r2t), r2t.stride(0), r2t.shape[0], _lib.ptr(rpi),
             _lib.ptr(positions), positions.stride(0), _lib.ptr(actual), bs, float(layer.scaling),
-            _lib.ptr(out), _lib.ptr(buf), buf.numel(), _lib.ptr(tickets), _lib.stream(q3.device),
+            _lib.ptr(out), _lib.ptr(buf), buf.numel(), _lib.stream(q3.device),
         )
         return out
 

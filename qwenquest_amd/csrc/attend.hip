@@ -15,11 +15,11 @@
 //        N, padded to 16); the S^T accumulator gives each lane one head and 4
 //        consecutive tokens, which is exactly the A-operand layout of
 //        v_mfma_f32_16x16x16bf16_1k, so P = exp(S - m) (bf16) feeds O = P V
-//        without an LDS round trip; V comes in 8-byte row pieces (4 channels)
-//        transposed 4x4 in registers, channel d = 64*half + 4*lane + e.
+//        without an LDS round trip; V comes in 16-byte row slices (8 channels)
+//        transposed 4x8 in registers, channel d = 8*(lane % 16) + e.
 //      Other shapes / fp32 use a scalar kernel with the same partial format.
 //   2. merge kernel, grid (H, bs): out = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c.
-#include "qq_common.h"
+#include "qq_kernels.h"
 
 namespace qq {
 namespace {
@@ -27,30 +27,7 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kChunk = 64;
 
-struct AttnArgs {
-  const void* q;
-  int q_dtype;
-  int64_t q_bstride;
-  int H;
-  const void* k;
-  const void* v;
-  int64_t kv_rows;
-  int KV, D;
-  const int32_t* r2t;
-  int64_t r2t_stride;
-  int64_t r2t_rows;
-  const int64_t* rpi;
-  const int32_t* positions;
-  const int64_t* rows;
-  int64_t pos_stride;
-  const int32_t* actual;
-  float scale;
-  void* out;
-  float* ws_o;   // [bs, max_chunks, H, D]
-  float* ws_ml;  // [bs, max_chunks, H, 2]
-  int max_chunks;
-  int32_t* tickets;
-};
+
 
 __device__ inline float ldkv(const uint16_t* p, int64_t i) { return bf2f(p[i]); }
 __device__ inline float ldkv(const float* p, int64_t i) { return p[i]; }
@@ -174,17 +151,15 @@ __global__ __launch_bounds__(64 * KV) void attn_mfma_kernel(AttnArgs a) {
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) ka[t][ks] = *reinterpret_cast<const bf16x8_t*>(kp + ks * 32);
   }
-  // V row pieces for P V: k-step s (16 tokens), half hf, token j of the lane's 4.
-  const uint16_t* vbase = static_cast<const uint16_t*>(a.v) + w * kMfmaDim + lo * 4;
-  uint2 vr[4][2][4];
+  // V row slices for P V: k-step s (16 tokens), token j of the lane's 4; 16 bytes =
+  // channels 8*lo .. 8*lo + 7 of this KV head (16 lanes cover the 256-byte slice).
+  const uint16_t* vbase = static_cast<const uint16_t*>(a.v) + w * kMfmaDim + lo * 8;
+  uint4 vr[4][4];
 #pragma unroll
   for (int s = 0; s < 4; ++s)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint16_t* vp = vbase + s_rows[s * 16 + hi * 4 + j] * kRow;
-#pragma unroll
-      for (int hf = 0; hf < 2; ++hf) vr[s][hf][j] = *reinterpret_cast<const uint2*>(vp + hf * 64);
-    }
+    for (int j = 0; j < 4; ++j)
+      vr[s][j] = *reinterpret_cast<const uint4*>(vbase + s_rows[s * 16 + hi * 4 + j] * kRow);
   // Q^T as the B operand: query head w*G + lo (zero past G), channels 8*hi + 32*ks.
   bf16x8_t qb[4];
   {
@@ -236,40 +211,35 @@ __global__ __launch_bounds__(64 * KV) void attn_mfma_kernel(AttnArgs a) {
   sum += __shfl_xor(sum, 16, 64);
   sum += __shfl_xor(sum, 32, 64);
 
-  // O[head 4*hi + i][d = 64*hf + 4*lo + e] in o[hf][e][i]
-  float4_t o[2][4];
+  // O[head 4*hi + i][d = 8*lo + e] in o[e][i]
+  float4_t o[8];
 #pragma unroll
-  for (int hf = 0; hf < 2; ++hf)
+  for (int e = 0; e < 8; ++e) o[e] = float4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int e = 0; e < 4; ++e) o[hf][e] = float4_t{0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < 4; ++s) {
+    short4_t vb[8];
 #pragma unroll
-  for (int s = 0; s < 4; ++s)
+    for (int j = 0; j < 4; ++j) {
+      const uint4 u = vr[s][j];
+      const uint32_t wv[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
-    for (int hf = 0; hf < 2; ++hf) {
-      short4_t vb[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint2 u = vr[s][hf][j];
-        vb[0][j] = (short)(u.x & 0xFFFFu);
-        vb[1][j] = (short)(u.x >> 16);
-        vb[2][j] = (short)(u.y & 0xFFFFu);
-        vb[3][j] = (short)(u.y >> 16);
+      for (int x = 0; x < 4; ++x) {
+        vb[2 * x][j] = (short)(wv[x] & 0xFFFFu);
+        vb[2 * x + 1][j] = (short)(wv[x] >> 16);
       }
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        o[hf][e] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa[s], vb[e], o[hf][e], 0, 0, 0);
     }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa[s], vb[e], o[e], 0, 0, 0);
+  }
 
   const int64_t part = (int64_t)b * a.max_chunks + c;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int head = hi * 4 + i;
     if (head < G) {
-      float* dst = a.ws_o + (part * a.H + w * G + head) * kMfmaDim + lo * 4;
-#pragma unroll
-      for (int hf = 0; hf < 2; ++hf)
-        *reinterpret_cast<float4*>(dst + hf * 64) =
-            make_float4(o[hf][0][i], o[hf][1][i], o[hf][2][i], o[hf][3][i]);
+      float* dst = a.ws_o + (part * a.H + w * G + head) * kMfmaDim + lo * 8;
+      *reinterpret_cast<float4*>(dst) = make_float4(o[0][i], o[1][i], o[2][i], o[3][i]);
+      *reinterpret_cast<float4*>(dst + 4) = make_float4(o[4][i], o[5][i], o[6][i], o[7][i]);
     }
   }
   if (hi == 0 && lo < G) {
@@ -279,62 +249,49 @@ __global__ __launch_bounds__(64 * KV) void attn_mfma_kernel(AttnArgs a) {
   }
 }
 
-// Combines the chunk partials of one (head, request): grid (H, bs).  The chunk
-// weights e^(m_c - M) / L are formed once in LDS; each thread then sums its
-// channels over the chunks with independent loads.
+// Combines the chunk partials of one (head, request): grid (H, bs), one thread
+// per channel.  Each thread issues the loads of up to 32 chunks' (m, l, o) at
+// once, then folds them with the online-softmax update
+// (M' = max(M, m_c), L = L e^(M - M') + l_c e^(m_c - M'), same for O).
 constexpr int kMaxChunks = 1024;
+constexpr int kMergeGroup = 32;
 
 __global__ __launch_bounds__(kThreads) void attn_merge_kernel(AttnArgs a) {
   const int h = blockIdx.x, b = blockIdx.y;
   const int n = (int)min((int64_t)a.actual[b], a.pos_stride);
-  const int nc = min((n + kChunk - 1) / kChunk, kMaxChunks);
-  const int64_t base = (int64_t)b * a.max_chunks;
+  const int nc = (n + kChunk - 1) / kChunk;
   const int H = a.H, D = a.D;
-  __shared__ float s_w[kMaxChunks];
-  __shared__ float s_red[kThreads / 64];
-  const int nthr = blockDim.x, nwaves = nthr >> 6;
-  // M = max_c m_c
-  float m = -INFINITY;
-  for (int cc = threadIdx.x; cc < nc; cc += nthr) {
-    const float mc = a.ws_ml[((base + cc) * H + h) * 2];
-    s_w[cc] = mc;
-    m = fmaxf(m, mc);
-  }
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-  if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = m;
-  __syncthreads();
-  float M = s_red[0];
-  for (int i = 1; i < nwaves; ++i) M = fmaxf(M, s_red[i]);
-  __syncthreads();
-  // L = sum_c e^(m_c - M) l_c ; s_w[c] = e^(m_c - M)
-  float lsum = 0.0f;
-  for (int cc = threadIdx.x; cc < nc; cc += nthr) {
-    const float e = expf(s_w[cc] - M);
-    s_w[cc] = e;
-    lsum += e * a.ws_ml[((base + cc) * H + h) * 2 + 1];
-  }
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) lsum += __shfl_xor(lsum, off, 64);
-  if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = lsum;
-  __syncthreads();
-  float L = 0.0f;
-  for (int i = 0; i < nwaves; ++i) L += s_red[i];
-  const float inv = nc > 0 ? 1.0f / L : 0.0f;
+  const int64_t base = (int64_t)b * a.max_chunks;
+  const float* ml = a.ws_ml + (base * H + h) * 2;
+  const int64_t mls = (int64_t)H * 2;
   const float* op = a.ws_o + (base * H + h) * D;
-  const int64_t cstride = (int64_t)H * D;
-  for (int d = threadIdx.x; d < D; d += nthr) {
-    float O = 0.0f;
-    int cc = 0;
-    for (; cc + 8 <= nc; cc += 8) {
-      float v[8];
+  const int64_t os = (int64_t)H * D;
+  for (int d = threadIdx.x; d < D; d += blockDim.x) {
+    float M = -INFINITY, L = 0.0f, O = 0.0f;
+    for (int c0 = 0; c0 < nc; c0 += kMergeGroup) {
+      float mv[kMergeGroup], lv[kMergeGroup], ov[kMergeGroup];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) v[u] = op[(cc + u) * cstride + d];
+      for (int u = 0; u < kMergeGroup; ++u) {
+        const bool ok = c0 + u < nc;
+        mv[u] = ok ? ml[(c0 + u) * mls] : -INFINITY;
+        lv[u] = ok ? ml[(c0 + u) * mls + 1] : 0.0f;
+        ov[u] = ok ? op[(c0 + u) * os + d] : 0.0f;
+      }
+      float gm = M;
 #pragma unroll
-      for (int u = 0; u < 8; ++u) O += s_w[cc + u] * v[u];
+      for (int u = 0; u < kMergeGroup; ++u) gm = fmaxf(gm, mv[u]);
+      const float sc = (M == -INFINITY) ? 0.0f : expf(M - gm);
+      L *= sc;
+      O *= sc;
+#pragma unroll
+      for (int u = 0; u < kMergeGroup; ++u) {
+        const float wgt = (mv[u] == -INFINITY) ? 0.0f : expf(mv[u] - gm);
+        L += wgt * lv[u];
+        O += wgt * ov[u];
+      }
+      M = gm;
     }
-    for (; cc < nc; ++cc) O += s_w[cc] * op[cc * cstride + d];
-    const float r = O * inv;
+    const float r = nc > 0 ? O / L : 0.0f;
     const int64_t oi = ((int64_t)b * H + h) * D + d;
     if (a.q_dtype == QQ_DTYPE_BF16)
       static_cast<uint16_t*>(a.out)[oi] = f2bf(r);
@@ -343,8 +300,49 @@ __global__ __launch_bounds__(kThreads) void attn_merge_kernel(AttnArgs a) {
   }
 }
 
+// Fast merge (nc <= 64 chunks, D a multiple of 64): lane c < nc loads (m_c,
+// l_c) of its chunk; wave reductions give M and L, the chunk weights e^(m_c - M)
+// go through LDS; every thread issued its channel's o_c loads before all that.
+__global__ __launch_bounds__(1024) void attn_merge64_kernel(AttnArgs a) {
+  const int h = blockIdx.x, b = blockIdx.y;
+  const int n = (int)min((int64_t)a.actual[b], a.pos_stride);
+  const int nc = (n + kChunk - 1) / kChunk;
+  const int H = a.H, D = a.D;
+  const int64_t base = (int64_t)b * a.max_chunks;
+  const int d = threadIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const float* op = a.ws_o + (base * H + h) * D + d;
+  const int64_t os = (int64_t)H * D;
+  float ov[64];
+#pragma unroll
+  for (int u = 0; u < 64; ++u) ov[u] = u < nc ? op[u * os] : 0.0f;
+  float2 ml = make_float2(-INFINITY, 0.0f);
+  if (lane < nc) ml = *reinterpret_cast<const float2*>(a.ws_ml + ((base + lane) * H + h) * 2);
+  float M = ml.x;
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+  const float wgt = lane < nc ? expf(ml.x - M) : 0.0f;
+  float L = wgt * ml.y;
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) L += __shfl_xor(L, off, 64);
+  __shared__ float s_w[16][64];
+  s_w[wave][lane] = wgt;
+  __syncthreads();
+  const float* w = s_w[wave];
+  float O = 0.0f;
+#pragma unroll
+  for (int u = 0; u < 64; ++u) O += w[u] * ov[u];
+  const float r = nc > 0 ? O / L : 0.0f;
+  const int64_t oi = ((int64_t)b * H + h) * D + d;
+  if (a.q_dtype == QQ_DTYPE_BF16)
+    static_cast<uint16_t*>(a.out)[oi] = f2bf(r);
+  else
+    static_cast<float*>(a.out)[oi] = r;
+}
+
+}  // namespace
+
 int launch_attention(AttnArgs& a, int kv_dtype, int bs, int64_t workspace_bytes, void* workspace,
-                     void* stream, const char* what) {
+                     hipStream_t s, const char* what) {
   const int64_t need = qq_decode_attention_workspace_bytes(bs, (int)a.pos_stride, a.H, a.D);
   QQ_REQUIRE(workspace && workspace_bytes >= need, "%s: workspace %lld bytes < %lld needed", what,
              (long long)workspace_bytes, (long long)need);
@@ -356,7 +354,6 @@ int launch_attention(AttnArgs& a, int kv_dtype, int bs, int64_t workspace_bytes,
   const size_t smem = kChunk * sizeof(int64_t) + (size_t)(a.H * a.D + a.H * kChunk + 2 * a.H) * 4;
   QQ_REQUIRE(smem <= 64 * 1024, "%s: %d heads x %d dims need too much LDS", what, a.H, a.D);
   dim3 grid(max(1, a.max_chunks), bs);
-  hipStream_t s = static_cast<hipStream_t>(stream);
   const int G = a.H / a.KV;
   const bool mfma = a.q_dtype == QQ_DTYPE_BF16 && kv_dtype == QQ_DTYPE_BF16 && a.D == kMfmaDim &&
                     G <= 16 && (a.KV == 1 || a.KV == 2 || a.KV == 4 || a.KV == 8);
@@ -372,18 +369,21 @@ int launch_attention(AttnArgs& a, int kv_dtype, int bs, int64_t workspace_bytes,
   } else {
     attn_chunk_kernel<float><<<grid, kThreads, smem, s>>>(a);
   }
-  attn_merge_kernel<<<dim3(a.H, bs), a.D <= 128 ? 128 : kThreads, 0, s>>>(a);
+  if (a.max_chunks <= 64 && a.D % 64 == 0 && a.D <= 1024)
+    attn_merge64_kernel<<<dim3(a.H, bs), a.D, 0, s>>>(a);
+  else
+    attn_merge_kernel<<<dim3(a.H, bs), a.D <= 128 ? 128 : kThreads, 0, s>>>(a);
   return check_launch(what);
 }
 
 int fill_common(AttnArgs& a, const void* q, int q_dtype, int64_t q_batch_stride, int num_q_heads,
                 const void* k_layer, const void* v_layer, int kv_dtype, int64_t kv_rows,
                 int kv_heads, int head_dim, const int32_t* actual_lens, float scale, void* out,
-                int32_t* tickets, const char* what) {
+                const char* what) {
   QQ_REQUIRE(dtype_ok(q_dtype) && dtype_ok(kv_dtype), "%s: unsupported dtype", what);
   QQ_REQUIRE(kv_heads > 0 && head_dim > 0 && num_q_heads > 0 && num_q_heads % kv_heads == 0,
              "%s: q_heads %d not divisible by kv_heads %d", what, num_q_heads, kv_heads);
-  QQ_REQUIRE(q && k_layer && v_layer && actual_lens && out && tickets, "%s: null pointer", what);
+  QQ_REQUIRE(q && k_layer && v_layer && actual_lens && out, "%s: null pointer", what);
   a.q = q;
   a.q_dtype = q_dtype;
   a.q_bstride = q_batch_stride;
@@ -396,7 +396,6 @@ int fill_common(AttnArgs& a, const void* q, int q_dtype, int64_t q_batch_stride,
   a.actual = actual_lens;
   a.scale = scale;
   a.out = out;
-  a.tickets = tickets;
   a.r2t = nullptr;
   a.r2t_stride = 0;
   a.r2t_rows = 0;
@@ -406,7 +405,6 @@ int fill_common(AttnArgs& a, const void* q, int q_dtype, int64_t q_batch_stride,
   return QQ_OK;
 }
 
-}  // namespace
 }  // namespace qq
 
 using namespace qq;
@@ -424,12 +422,12 @@ extern "C" int qq_quest_decode_attention(const void* q, int q_dtype, int64_t q_b
                                          int64_t req_to_token_rows, const int64_t* req_pool_indices, const int32_t* positions,
                                          int64_t positions_stride, const int32_t* actual_lens,
                                          int bs, float scale, void* out, void* workspace,
-                                         int64_t workspace_bytes, int32_t* tickets, void* stream) {
+                                         int64_t workspace_bytes, void* stream) {
   const char* what = "qq_quest_decode_attention";
   if (bs == 0) return QQ_OK;
   AttnArgs a;
   int st = fill_common(a, q, q_dtype, q_batch_stride, num_q_heads, k_layer, v_layer, kv_dtype,
-                       kv_rows, kv_heads, head_dim, actual_lens, scale, out, tickets, what);
+                       kv_rows, kv_heads, head_dim, actual_lens, scale, out, what);
   if (st != QQ_OK) return st;
   QQ_REQUIRE(req_to_token && req_pool_indices && positions && positions_stride > 0,
              "%s: null row map", what);
@@ -439,7 +437,7 @@ extern "C" int qq_quest_decode_attention(const void* q, int q_dtype, int64_t q_b
   a.rpi = req_pool_indices;
   a.positions = positions;
   a.pos_stride = positions_stride;
-  return launch_attention(a, kv_dtype, bs, workspace_bytes, workspace, stream, what);
+  return launch_attention(a, kv_dtype, bs, workspace_bytes, workspace, static_cast<hipStream_t>(stream), what);
 }
 
 extern "C" int qq_decode_attention_rows(const void* q, int q_dtype, int64_t q_batch_stride,
@@ -447,16 +445,15 @@ extern "C" int qq_decode_attention_rows(const void* q, int q_dtype, int64_t q_ba
                                         int kv_dtype, int64_t kv_rows, int kv_heads, int head_dim,
                                         const int64_t* rows, int64_t rows_stride,
                                         const int32_t* actual_lens, int bs, float scale, void* out,
-                                        void* workspace, int64_t workspace_bytes, int32_t* tickets,
-                                        void* stream) {
+                                        void* workspace, int64_t workspace_bytes, void* stream) {
   const char* what = "qq_decode_attention_rows";
   if (bs == 0) return QQ_OK;
   AttnArgs a;
   int st = fill_common(a, q, q_dtype, q_batch_stride, num_q_heads, k_layer, v_layer, kv_dtype,
-                       kv_rows, kv_heads, head_dim, actual_lens, scale, out, tickets, what);
+                       kv_rows, kv_heads, head_dim, actual_lens, scale, out, what);
   if (st != QQ_OK) return st;
   QQ_REQUIRE(rows && rows_stride > 0, "%s: null row list", what);
   a.rows = rows;
   a.pos_stride = rows_stride;
-  return launch_attention(a, kv_dtype, bs, workspace_bytes, workspace, stream, what);
+  return launch_attention(a, kv_dtype, bs, workspace_bytes, workspace, static_cast<hipStream_t>(stream), what);
 }

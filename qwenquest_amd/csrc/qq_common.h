@@ -69,15 +69,6 @@ inline bool dtype_ok(int dtype) { return dtype == QQ_DTYPE_BF16 || dtype == QQ_D
 
 inline int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
 
-// Agent-scope acquire/release helpers for the "last workgroup finishes" pattern.
-// A release fence + agent-scope atomic makes this workgroup's global writes
-// visible to the workgroup that observes the final ticket, across XCD L2s.
-__device__ inline int ticket_arrive(int* ticket) {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-  return __hip_atomic_fetch_add(ticket, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ inline void acquire_fence() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent"); }
-
 }  // namespace qq
 
 #define QQ_REQUIRE(cond, ...)                                  \

@@ -3,8 +3,9 @@
 // Reference: src/qwenquest/quest.py:366-464 (group_queries, page_scores,
 // retrieve_topk) and the layout of prepare_step (quest.py:333-342).
 //
-// Launch 1, grid (page blocks, bs): each block averages q over the GQA group,
-// then its 4 waves score candidate pages [0, candidate_limit): lane l holds
+// Launch 1, grid (page blocks, bs): each block averages q over the GQA group
+// (once, into LDS) while its 4 waves' page loads are in flight; each wave then
+// scores 8 candidate pages of [0, candidate_limit): lane l holds
 // channels [l*m, l*m + m) of the page (m = ceil(KV*D / 64)), so a wave reads a
 // page's KV*D (min, max) words as one coalesced 2 KiB stream at KV*D = 512.
 // Per page the lane adds its m fp32 products in channel order and the 64 lane
@@ -16,7 +17,7 @@
 // per-thread maxima filters the keys, survivors are rank-counted; otherwise a 4-pass radix
 // select on order-preserving 32-bit keys with ties at the threshold to the
 // lowest page index.
-#include "qq_common.h"
+#include "qq_kernels.h"
 
 namespace qq {
 namespace {
@@ -27,20 +28,37 @@ constexpr int kMaxC = 1024;    // KV * D
 constexpr int kMaxSel = 1024;  // top_k / P - 1
 constexpr int kPagesPerBlock = 32;
 
-struct SelectArgs {
-  const void* q;
-  int q_dtype;
-  int64_t q_bstride;
-  int H;
-  const uint32_t* bounds_layer;  // [R, MP, C] (min, max) words of this layer
-  const int64_t* rpi;
-  const int64_t* seq;
-  const int32_t* limit;
-  int R, MP, KV, D, C, m, P, top_k, k_sel, ppb;
-  float* scores;
-  int32_t* tickets;
-  int32_t* positions;
-};
+
+
+// k_pool[new_locs[b]] = new_k[b] (and V), one row of C elements, converted to the pool dtype.
+__device__ inline void store_new_token(const SelectArgs& a, int b) {
+  if (!a.new_k) return;
+  const int64_t loc = a.new_locs[b];
+  if (loc < 0 || loc >= a.pool_rows) return;
+  const int C = a.C;
+  if (a.new_dtype == QQ_DTYPE_BF16 && a.pool_dtype == QQ_DTYPE_BF16 && C % 8 == 0) {
+    const uint4* ks = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.new_k) + (int64_t)b * C);
+    const uint4* vs = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.new_v) + (int64_t)b * C);
+    uint4* kd = reinterpret_cast<uint4*>(static_cast<uint16_t*>(a.k_pool) + loc * C);
+    uint4* vd = reinterpret_cast<uint4*>(static_cast<uint16_t*>(a.v_pool) + loc * C);
+    for (int e = threadIdx.x; e < C / 8; e += blockDim.x) {
+      kd[e] = ks[e];
+      vd[e] = vs[e];
+    }
+    return;
+  }
+  for (int e = threadIdx.x; e < C; e += blockDim.x) {
+    const float kv = load_as_float(a.new_k, (int64_t)b * C + e, a.new_dtype);
+    const float vv = load_as_float(a.new_v, (int64_t)b * C + e, a.new_dtype);
+    if (a.pool_dtype == QQ_DTYPE_BF16) {
+      static_cast<uint16_t*>(a.k_pool)[loc * C + e] = f2bf(kv);
+      static_cast<uint16_t*>(a.v_pool)[loc * C + e] = f2bf(vv);
+    } else {
+      static_cast<float*>(a.k_pool)[loc * C + e] = kv;
+      static_cast<float*>(a.v_pool)[loc * C + e] = vv;
+    }
+  }
+}
 
 __device__ inline void write_recent(int32_t* pos, int64_t s, int P) {
   const int64_t start = max(s - P, (int64_t)0);
@@ -164,42 +182,39 @@ __device__ inline void load_lane_words(uint32_t (&w)[M], const uint32_t* pb, int
   }
 }
 
-// q-bar of this lane's channels c = lane*m + j, in registers (no LDS, no barrier).
-template <int M>
-__device__ inline void lane_qbar(float (&qreg)[M], const void* q, int dtype, int64_t qb, int G,
-                                 int D, int m, int C, int lane) {
-  if (dtype == QQ_DTYPE_BF16 && M == 8 && m == 8 && D % 8 == 0 && G > 1) {
-    const int c0 = lane * 8;
-    if (c0 >= C) {
+// q-bar of channels [0, C) into LDS, computed once per block (each thread a
+// channel pair when the query is bf16 and D is even: G 4-byte loads).
+__device__ inline void block_qbar(float* s_q, const SelectArgs& a, int b) {
+  const int G = a.H / a.KV;
+  const int64_t qb = (int64_t)b * a.q_bstride;
+  constexpr int kMaxG = 16;
+  if (a.q_dtype == QQ_DTYPE_BF16 && a.D % 2 == 0 && G > 1 && G <= kMaxG) {
+    for (int c = threadIdx.x * 2; c < a.C; c += kThreads * 2) {
+      const int h = c / a.D, d = c - h * a.D;
+      const uint32_t* qp =
+          reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(a.q) + qb + (int64_t)h * G * a.D + d);
+      uint32_t u[kMaxG];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) qreg[j] = 0.0f;
-      return;
-    }
-    const int h = c0 / D, d0 = c0 - h * D;
-    float acc[8];
+      for (int g = 0; g < kMaxG; ++g) u[g] = g < G ? qp[(int64_t)g * (a.D / 2)] : 0u;  // all in flight
+      float a0 = 0.0f, a1 = 0.0f;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
-    const uint16_t* qp = static_cast<const uint16_t*>(q) + qb + (int64_t)h * G * D + d0;
-    for (int g = 0; g < G; ++g) {
-      const uint4 u = *reinterpret_cast<const uint4*>(qp + (int64_t)g * D);
-      const uint32_t wv[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        acc[2 * j] = __fadd_rn(acc[2 * j], bf2f((uint16_t)(wv[j] & 0xFFFFu)));
-        acc[2 * j + 1] = __fadd_rn(acc[2 * j + 1], bf2f((uint16_t)(wv[j] >> 16)));
+      for (int g = 0; g < kMaxG; ++g) {
+        if (g < G) {
+          a0 = __fadd_rn(a0, bf2f((uint16_t)(u[g] & 0xFFFFu)));
+          a1 = __fadd_rn(a1, bf2f((uint16_t)(u[g] >> 16)));
+        }
       }
+      s_q[c] = bf2f(f2bf(a0 / (float)G));
+      s_q[c + 1] = bf2f(f2bf(a1 / (float)G));
     }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) qreg[j] = bf2f(f2bf(acc[j] / (float)G));
     return;
   }
-#pragma unroll
-  for (int j = 0; j < M; ++j) {
-    const int c = lane * m + j;
-    qreg[j] = (j < m && c < C) ? gqa_mean(q, dtype, qb, G, D, c) : 0.0f;
-  }
+  for (int c = threadIdx.x; c < a.C; c += kThreads) s_q[c] = gqa_mean(a.q, a.q_dtype, qb, G, a.D, c);
 }
 
+// Scores the candidate pages [0, candidate_limit) of long requests: each wave
+// 8 pages.  The bounds loads are issued first; q-bar is then computed once per
+// block into LDS while they are in flight (the barrier does not wait for them).
 template <int M>
 __global__ __launch_bounds__(kThreads) void score_candidates_kernel(SelectArgs a) {
   const int b = blockIdx.y;
@@ -212,14 +227,21 @@ __global__ __launch_bounds__(kThreads) void score_candidates_kernel(SelectArgs a
   if (req < 0 || req >= a.R) return;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int pw = p0 + wave * 8;  // this wave's 8 pages
-  if (pw >= lim) return;
   const uint32_t* pbase = a.bounds_layer + req * a.MP * a.C;
   uint32_t w[8][M];
 #pragma unroll
   for (int i = 0; i < 8; ++i)
     load_lane_words<M>(w[i], pbase + (int64_t)(pw + i) * a.C, lane, a.m, a.C, pw + i < lim);
+  __shared__ float s_q[kMaxC];
+  block_qbar(s_q, a, b);
+  __syncthreads();
+  if (pw >= lim) return;
   float qreg[M];
-  lane_qbar<M>(qreg, a.q, a.q_dtype, (int64_t)b * a.q_bstride, a.H / a.KV, a.D, a.m, a.C, lane);
+#pragma unroll
+  for (int j = 0; j < M; ++j) {
+    const int c = lane * a.m + j;
+    qreg[j] = (j < a.m && c < a.C) ? s_q[c] : 0.0f;
+  }
   float acc[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = lane_partial<M>(w[i], qreg, lane, a.m, a.C);
@@ -232,6 +254,7 @@ __global__ __launch_bounds__(kThreads) void score_candidates_kernel(SelectArgs a
 __global__ __launch_bounds__(kThreads) void select_layout_kernel(SelectArgs a) {
   const int b = blockIdx.x;
   const int tid = threadIdx.x;
+  store_new_token(a, b);
   const int64_t s = a.seq[b];
   int32_t* pos = a.positions + (int64_t)b * a.top_k;
   if (s <= a.top_k) {  // dense layout, quest.py:339-342 / 460
@@ -341,19 +364,21 @@ __device__ inline uint64_t sel_key(uint32_t score_key, int page) {
   return ((uint64_t)score_key << 32) | (uint32_t)(~(uint32_t)page);
 }
 
-// Top k <= 64 pages of n_eff <= 256*KPT keys, one block per request, no atomics
-// on hot bins and no long dependent shuffle chains:
+// Top k <= 64 pages of n_eff <= 256*KPT keys, one block per request:
 //   1. each thread holds KPT keys (pages tid + 256 i) and their max;
-//   2. T0 = the k-th largest of the 256 thread maxima (LDS rank counting).  The
-//      k largest maxima are k distinct keys >= T0, so the true k-th largest key
-//      is >= T0 and every top-k key survives the filter key >= T0;
-//   3. survivors are compacted into LDS (ballot + mbcnt per wave);
+//   2. per wave, T_w = the k-th largest of its 64 lane maxima (LDS rank
+//      counting; 0 if fewer than k lanes hold keys).  The k largest lane maxima
+//      are k distinct keys >= T_w, so the true k-th largest key is >= T_w, and
+//      every top-k key survives the filter key >= T0 = max_w T_w;
+//   3. each wave compacts its survivors into its own LDS region (ballot +
+//      mbcnt, running base kept in a scalar register: no atomics);
 //   4. each survivor's rank = number of survivors above it; ranks < k give the
 //      pages in (score desc, page asc) order.
 template <int KPT>
 __global__ __launch_bounds__(kThreads) void select_filter_kernel(SelectArgs a) {
   const int b = blockIdx.x;
   const int tid = threadIdx.x;
+  store_new_token(a, b);
   const int64_t s = a.seq[b];
   int32_t* pos = a.positions + (int64_t)b * a.top_k;
   if (s <= a.top_k) {
@@ -370,51 +395,65 @@ __global__ __launch_bounds__(kThreads) void select_filter_kernel(SelectArgs a) {
   const int n_eff = max(lim, k);
   const float* sc = a.scores + (int64_t)b * a.MP;
   constexpr uint32_t kNegInfKey = 0x007FFFFFu;  // orderable(-inf): masked pages (quest.py:451)
+  const int wave = tid >> 6, lane = tid & 63;
 
+  float sv[KPT];
+#pragma unroll
+  for (int i = 0; i < KPT; ++i) {
+    const int p = tid + kThreads * i;
+    sv[i] = p < lim ? sc[p] : 0.0f;
+  }
   uint64_t key[KPT];
   uint64_t tmax = 0ull;
 #pragma unroll
   for (int i = 0; i < KPT; ++i) {
     const int p = tid + kThreads * i;
-    key[i] = p < n_eff ? sel_key(p < lim ? orderable(sc[p]) : kNegInfKey, p) : 0ull;
+    key[i] = p < n_eff ? sel_key(p < lim ? orderable(sv[i]) : kNegInfKey, p) : 0ull;
     tmax = key[i] > tmax ? key[i] : tmax;
   }
   __shared__ uint64_t s_max[kThreads];
-  __shared__ uint64_t s_cand[kThreads * KPT];
-  __shared__ uint64_t s_t0;
-  __shared__ int s_nz, s_nc;
+  __shared__ uint64_t s_tw[kWaves];
+  __shared__ uint64_t s_cand[kWaves][64 * KPT];
+  __shared__ int s_cnt[kWaves];
   __shared__ int s_order[64];
-  if (tid == 0) {
-    s_t0 = 0ull;
-    s_nz = 0;
-    s_nc = 0;
-  }
   s_max[tid] = tmax;
+  const int nz = __popcll(__ballot(tmax != 0ull));
+  if (lane == 0) s_tw[wave] = 0ull;
   __syncthreads();
-  if (tmax != 0ull) atomicAdd(&s_nz, 1);
   int rank = 0;
-  for (int j = 0; j < kThreads; ++j) rank += s_max[j] > tmax;
+#pragma unroll 16
+  for (int j = 0; j < 64; ++j) rank += s_max[wave * 64 + j] > tmax;
+  if (nz >= k && tmax != 0ull && rank == k - 1) s_tw[wave] = tmax;  // unique: nonzero keys differ
   __syncthreads();
-  if (s_nz >= k && tmax != 0ull && rank == k - 1) s_t0 = tmax;  // unique: nonzero keys differ
-  __syncthreads();
-  const uint64_t t0 = s_t0;
-  const int lane = tid & 63;
+  uint64_t t0 = s_tw[0];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) t0 = s_tw[w] > t0 ? s_tw[w] : t0;
+  int base = 0;
 #pragma unroll
   for (int i = 0; i < KPT; ++i) {
     const bool take = key[i] != 0ull && key[i] >= t0;
     const uint64_t mask = __ballot(take);
-    int base = 0;
-    if (lane == 0 && mask) base = atomicAdd(&s_nc, __popcll(mask));
-    base = __shfl(base, 0, 64);
-    if (take) s_cand[base + __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
-                                                      __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u))] = key[i];
+    if (take)
+      s_cand[wave][base + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
+                                                         __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u))] = key[i];
+    base += __popcll(mask);
   }
+  if (lane == 0) s_cnt[wave] = base;
   __syncthreads();
-  const int nc = s_nc;
-  for (int i = tid; i < nc; i += kThreads) {
-    const uint64_t ci = s_cand[i];
+  int cnt[kWaves], total = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    cnt[w] = s_cnt[w];
+    total += cnt[w];
+  }
+  for (int i = tid; i < total; i += kThreads) {
+    int w0 = 0, off = i;
+    while (off >= cnt[w0]) off -= cnt[w0++];
+    const uint64_t ci = s_cand[w0][off];
     int r = 0;
-    for (int j = 0; j < nc; ++j) r += s_cand[j] > ci;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w)
+      for (int j = 0; j < cnt[w]; ++j) r += s_cand[w][j] > ci;
     if (r < k) s_order[r] = (int)(~(uint32_t)ci);
   }
   __syncthreads();
@@ -472,6 +511,38 @@ __global__ __launch_bounds__(kThreads) void page_scores_kernel(const void* qbar,
 }
 
 }  // namespace
+
+static void launch_select(const SelectArgs& a, int bs, int max_pages, int k_sel, hipStream_t s) {
+  const int n_max = max(max_pages, k_sel);
+  if (k_sel <= 64 && n_max <= 4 * kThreads)
+    select_filter_kernel<4><<<bs, kThreads, 0, s>>>(a);
+  else if (k_sel <= 64 && n_max <= 8 * kThreads)
+    select_filter_kernel<8><<<bs, kThreads, 0, s>>>(a);
+  else if (k_sel <= 64 && n_max <= 12 * kThreads)
+    select_filter_kernel<12><<<bs, kThreads, 0, s>>>(a);
+  else if (k_sel <= 64 && n_max <= 16 * kThreads)
+    select_filter_kernel<16><<<bs, kThreads, 0, s>>>(a);
+  else
+    select_layout_kernel<<<bs, kThreads, 0, s>>>(a);
+}
+
+int launch_retrieve(const SelectArgs& a, int bs, hipStream_t s) {
+  dim3 grid(max(1, ceil_div(a.MP, kPagesPerBlock)), bs);
+  const int M = (a.C + 63) / 64;
+  if (M <= 1)
+    score_candidates_kernel<1><<<grid, kThreads, 0, s>>>(a);
+  else if (M <= 2)
+    score_candidates_kernel<2><<<grid, kThreads, 0, s>>>(a);
+  else if (M <= 4)
+    score_candidates_kernel<4><<<grid, kThreads, 0, s>>>(a);
+  else if (M <= 8)
+    score_candidates_kernel<8><<<grid, kThreads, 0, s>>>(a);
+  else
+    score_candidates_kernel<16><<<grid, kThreads, 0, s>>>(a);
+  launch_select(a, bs, a.MP, a.k_sel, s);
+  return check_launch("quest retrieve");
+}
+
 }  // namespace qq
 
 using namespace qq;
@@ -528,7 +599,7 @@ extern "C" int qq_quest_retrieve_topk(const void* q, int q_dtype, int64_t q_batc
                                       const int64_t* req_pool_indices, const int64_t* seq_lens,
                                       const int32_t* candidate_limit, int bs, int max_reqs,
                                       int max_pages, int kv_heads, int head_dim, int page_size,
-                                      int top_k, float* scores_ws, int32_t* tickets,
+                                      int top_k, float* scores_ws,
                                       int32_t* positions, void* stream) {
   QQ_REQUIRE(dtype_ok(q_dtype), "qq_quest_retrieve_topk: unsupported query dtype %d", q_dtype);
   QQ_REQUIRE(kv_heads > 0 && head_dim > 0 && num_q_heads > 0, "qq_quest_retrieve_topk: bad heads");
@@ -564,27 +635,9 @@ extern "C" int qq_quest_retrieve_topk(const void* q, int q_dtype, int64_t q_batc
   a.k_sel = k_sel;
   a.ppb = kPagesPerBlock;
   a.scores = scores_ws;
-  a.tickets = tickets;
   a.positions = positions;
-  dim3 grid(max(1, ceil_div(max_pages, kPagesPerBlock)), bs);
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const int M = (C + 63) / 64;
-  if (M <= 1)
-    score_candidates_kernel<1><<<grid, kThreads, 0, s>>>(a);
-  else if (M <= 2)
-    score_candidates_kernel<2><<<grid, kThreads, 0, s>>>(a);
-  else if (M <= 4)
-    score_candidates_kernel<4><<<grid, kThreads, 0, s>>>(a);
-  else if (M <= 8)
-    score_candidates_kernel<8><<<grid, kThreads, 0, s>>>(a);
-  else
-    score_candidates_kernel<16><<<grid, kThreads, 0, s>>>(a);
-  const int n_max = max(max_pages, k_sel);
-  if (k_sel <= 64 && n_max <= 8 * kThreads)
-    select_filter_kernel<8><<<bs, kThreads, 0, s>>>(a);
-  else if (k_sel <= 64 && n_max <= 16 * kThreads)
-    select_filter_kernel<16><<<bs, kThreads, 0, s>>>(a);
-  else
-    select_layout_kernel<<<bs, kThreads, 0, s>>>(a);
+  a.new_k = nullptr;
+  const int st = launch_retrieve(a, bs, static_cast<hipStream_t>(stream));
+  if (st != QQ_OK) return st;
   return check_launch("qq_quest_retrieve_topk");
 }

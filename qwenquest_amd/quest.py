@@ -160,9 +160,8 @@ class QuestAlgorithm:
         self.running_k_max = torch.empty(rshape, dtype=torch.bfloat16, device=dev)
         self.running_token_count = torch.empty(max_reqs, dtype=torch.int32, device=dev)
         self.running_page_idx = torch.empty(max_reqs, dtype=torch.int32, device=dev)
-        # per-call workspaces of retrieve_topk: page scores + per-request tickets
+        # per-call workspace of retrieve_topk: the page scores of the batch
         self._scores_ws = torch.empty((max_reqs, max(self.max_pages_per_req, 1)), dtype=torch.float32, device=dev)
-        self._tickets = torch.zeros(max_reqs, dtype=torch.int32, device=dev)
         self._reset(0, max_reqs)
         self._initialized = True
 
@@ -388,8 +387,7 @@ class QuestAlgorithm:
             _lib.ptr(self.page_k_bounds), layer_id - self.start_layer, _lib.ptr(rpi),
             _lib.ptr(step.seq_lens), _lib.ptr(step.candidate_limit_i32), bs, self.max_reqs,
             self.max_pages_per_req, self.kv_heads, self.head_dim, self.page_size, self.top_k,
-            _lib.ptr(self._scores_ws), _lib.ptr(self._tickets), _lib.ptr(positions),
-            _lib.stream(self.device),
+            _lib.ptr(self._scores_ws), _lib.ptr(positions), _lib.stream(self.device),
         )
         if self.trace is not None:
             self._record(layer_id, rpi, step, positions[:bs])
