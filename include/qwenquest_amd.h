@@ -191,6 +191,71 @@ int qq_kv_scatter(void* k_layer, void* v_layer, int buf_dtype, int64_t kv_rows, 
                   const void* v, int src_dtype, const int64_t* locs, int n, int64_t row_elems,
                   void* stream);
 
+/* ------------------------------------------------------------- HiSparse tier
+ * Layouts of the reference HiSparseCoordinator (src/qwenquest/hisparse/coordinator.py:103-131):
+ * device_k/v[layer] [R*(buf+1), KV, D] (request r owns rows r*(buf+1) + slot,
+ * slot buf = newest token), buffer_tokens/lru_slots [L, R, buf] int64,
+ * req_to_host_pool [R, max_ctx] int64 (-1 = none), host_k/v[layer]
+ * [host_rows, KV, D] in pinned host memory that the kernels read and write
+ * directly (device-accessible pointer from qq_host_device_pointer). */
+
+/* Replaces HiSparseCoordinator.swap_in_selected_pages / _swap_in_long
+ * (coordinator.py:232-304) for one layer: rows_out [bs, top_k] int64 (-1 past
+ * actual_lens) index device_k/v of the layer; misses are loaded from the host
+ * tier into the least recently used slots (deduplicated by first occurrence),
+ * buffer_tokens / lru_slots of the layer are updated exactly as the reference
+ * does, stats[0..2] += (hits, misses, fast-path calls).  copy_dst/copy_src
+ * [bs, top_k] int64 and copy_count [bs] int32 are workspaces.  Too few victims
+ * (coordinator.py:278-279) sets bit 1 of *error_flags, a missing host row
+ * (:285-286) bit 2; that request is then left unchanged. */
+int qq_hisparse_swap_in(const int32_t* positions, int64_t positions_stride,
+                        const int32_t* actual_lens, const int64_t* seq_lens,
+                        const int64_t* req_pool_indices, int bs, int max_reqs,
+                        int device_buffer_size, int top_k, int64_t* buffer_tokens_layer,
+                        int64_t* lru_slots_layer, const int64_t* req_to_host_pool,
+                        int64_t max_context_len, void* device_k_layer, void* device_v_layer,
+                        const void* host_k_layer, const void* host_v_layer, int64_t row_bytes,
+                        int64_t host_rows, int64_t* rows_out, int64_t* copy_dst,
+                        int64_t* copy_src, int32_t* copy_count, uint64_t* stats,
+                        int32_t* error_flags, void* stream);
+
+/* Row copies over n_layers layers: dst[layer][dst_idx[i]] = src[layer][src_idx[i]]
+ * (row_bytes each; indices outside [0, rows) are skipped).  Carries the
+ * admission copies (coordinator.py:158-164: token pool -> host tier and hot
+ * buffer) and the eager backup (coordinator.py:211-215: hot buffer -> host). */
+int qq_copy_rows(const void* src, int64_t src_layer_stride_bytes, int64_t src_rows,
+                 const int64_t* src_idx, void* dst, int64_t dst_layer_stride_bytes,
+                 int64_t dst_rows, const int64_t* dst_idx, int n, int n_layers,
+                 int64_t row_bytes, void* stream);
+
+/* Per-request LRU state.  release == 0 (admit, coordinator.py:155, 166-167):
+ * buffer_tokens[:, req, s] = s, lru_slots[:, req, s] = s, req_to_host_pool[req, :n]
+ * = host_idx, the rest -1.  release != 0 (coordinator.py:312-314):
+ * buffer_tokens = -1, lru_slots = identity, req_to_host_pool[req] = -1. */
+int qq_hisparse_request_state(int64_t* buffer_tokens, int64_t* lru_slots, int num_layers,
+                              int max_reqs, int device_buffer_size, int64_t* req_to_host_pool,
+                              int64_t max_context_len, int req, const int64_t* host_idx, int64_t n,
+                              int release, void* stream);
+
+/* Eager-backup bookkeeping (coordinator.py:201-212): for listed request i with
+ * previous position seq_lens[i]-2, device_rows[i] = req*(buf+1) + min(seq-2, buf)
+ * and req_to_host_pool[req, seq-2] = host_idx[i]. */
+int qq_hisparse_backup_index(const int64_t* req_indices, const int64_t* seq_lens,
+                             const int64_t* host_idx, int n, int device_buffer_size, int max_reqs,
+                             int64_t* req_to_host_pool, int64_t max_context_len,
+                             int64_t* device_rows, void* stream);
+
+/* Replaces HiSparseCoordinator.write_new_token (coordinator.py:217-228): the new
+ * K/V of request i goes to hot-buffer slot min(seq_lens[i]-1, buf). */
+int qq_hisparse_write_new_token(void* device_k_layer, void* device_v_layer, int buf_dtype,
+                                const void* k, const void* v, int src_dtype,
+                                const int64_t* req_pool_indices, const int64_t* seq_lens, int bs,
+                                int device_buffer_size, int max_reqs, int64_t row_elems,
+                                void* stream);
+
+/* Device-side address of pinned host memory (hipHostGetDevicePointer). */
+int qq_host_device_pointer(void* host_ptr, void** device_ptr);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,8 +1,9 @@
 """Attention backends (reference ``src/qwenquest/attention/__init__.py``)."""
 
 from qwenquest_amd.attention.base import AttentionBackend
+from qwenquest_amd.attention.quest_hisparse import QuestHiSparseBackend
 from qwenquest_amd.attention.quest_only import QuestOnlyBackend
 
 ATTENTION_MODES = ("quest", "quest_hisparse")
 
-__all__ = ["ATTENTION_MODES", "AttentionBackend", "QuestOnlyBackend"]
+__all__ = ["ATTENTION_MODES", "AttentionBackend", "QuestHiSparseBackend", "QuestOnlyBackend"]

@@ -1,0 +1,542 @@
+// HiSparse hierarchical KV cache (Quest mode): pinned host tier + per-request
+// LRU hot buffer on the GPU.
+//
+// Reference: src/qwenquest/hisparse/coordinator.py (HiSparseCoordinator).
+// Layouts (reference coordinator.py:103-131):
+//   device_k/v[layer]  [R*(buf+1), KV, D]; request r owns rows r*(buf+1) + slot,
+//                      slot buf is the reserved newest-token slot
+//   buffer_tokens      [L, R, buf] int64  position cached by each LRU slot (-1 none)
+//   lru_slots          [L, R, buf] int64  slots, least -> most recently used
+//   req_to_host_pool   [R, max_ctx] int64 host row of each position (-1 none)
+//   host_k/v[layer]    [host_pool+1, KV, D] in pinned host memory, read and
+//                      written by the kernels directly over PCIe (zero-copy)
+//
+// Swap-in, one block of 1024 threads per request (coordinator.py:232-304):
+//   fast path seq <= buf: row = base + position;
+//   otherwise the newest position maps to the reserved slot; the others are
+//   deduplicated by first occurrence (LDS hash table, atomicMin of the entry
+//   index); every LRU slot's token is looked up in the table (hits); misses =
+//   first occurrences without a hit, ranked in entry order; evictable = LRU
+//   entries that are not hits, ranked in LRU order; miss r goes to evictable r;
+//   the LRU becomes [evictable[m:], victims, hits]; each entry (duplicates
+//   included) reads its position's slot from the table.  Both error conditions
+//   of the reference (too few victims, coordinator.py:278-279; a position
+//   without host backup, :285-286) are detected before any state is written
+//   and reported through a device error word.  A second grid-wide kernel then
+//   copies the missed rows host -> device.
+#include "qq_common.h"
+
+namespace qq {
+namespace {
+
+constexpr int kPlanThreads = 1024;
+constexpr int kPlanWaves = kPlanThreads / 64;
+constexpr int kMaxPerThread = 8;  // buf <= 8192, top_k <= 8192 entries per thread loop bound
+constexpr int kEmpty = -1;
+constexpr int kErrVictims = 1;
+constexpr int kErrHostRow = 2;
+
+struct SwapArgs {
+  const int32_t* positions;
+  int64_t pos_stride;
+  const int32_t* actual;
+  const int64_t* seq;
+  const int64_t* rpi;
+  int64_t* tokens;  // [R, buf] of this layer
+  int64_t* lru;     // [R, buf] of this layer
+  const int64_t* r2h;
+  int64_t r2h_stride;
+  int R, buf, top_k;
+  int64_t* rows_out;
+  int64_t rows_stride;
+  int64_t* copy_dst;  // [bs, top_k]
+  int64_t* copy_src;
+  int32_t* copy_count;  // [bs]
+  unsigned long long* stats;  // hits, misses, fast_path_calls
+  int32_t* err;
+  int table_size;  // power of two >= 2 * top_k
+};
+
+__device__ inline uint32_t slot_hash(int p, int mask) {
+  return ((uint32_t)p * 2654435761u >> 7) & (uint32_t)mask;
+}
+
+__device__ inline int table_find(const int* keys, int p, int mask) {
+  uint32_t h = slot_hash(p, mask);
+  for (int probe = 0; probe <= mask; ++probe) {
+    const int k = keys[h];
+    if (k == p) return (int)h;
+    if (k == kEmpty) return -1;
+    h = (h + 1) & (uint32_t)mask;
+  }
+  return -1;
+}
+
+// Exclusive block scan of one int per thread; returns the prefix, *total = sum.
+__device__ inline int block_scan(int v, int* s_wave, int* total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int x = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(x, off, 64);
+    if (lane >= off) x += y;
+  }
+  if (lane == 63) s_wave[wave] = x;
+  __syncthreads();
+  int wave_base = 0, sum = 0;
+  for (int w = 0; w < kPlanWaves; ++w) {
+    const int t = s_wave[w];
+    if (w < wave) wave_base += t;
+    sum += t;
+  }
+  __syncthreads();
+  *total = sum;
+  return wave_base + x - v;
+}
+
+__global__ __launch_bounds__(kPlanThreads) void swap_plan_kernel(SwapArgs a) {
+  extern __shared__ __align__(16) int smem[];
+  const int b = blockIdx.x, tid = threadIdx.x;
+  const int64_t req = a.rpi[b];
+  const int64_t s = a.seq[b];
+  const int buf = a.buf;
+  const int n = (int)min((int64_t)a.actual[b], min(a.pos_stride, (int64_t)a.top_k));
+  int64_t* rows = a.rows_out + (int64_t)b * a.rows_stride;
+  const int32_t* pos = a.positions + (int64_t)b * a.pos_stride;
+  if (req < 0 || req >= a.R) {
+    for (int i = tid; i < a.top_k; i += kPlanThreads) rows[i] = -1;
+    if (tid == 0) a.copy_count[b] = 0;
+    return;
+  }
+  const int64_t base_row = req * (int64_t)(buf + 1);
+  if (s <= buf) {  // fast path: the whole sequence is resident, slot == position
+    for (int i = tid; i < a.top_k; i += kPlanThreads) rows[i] = i < n ? base_row + pos[i] : -1;
+    if (tid == 0) {
+      a.copy_count[b] = 0;
+      atomicAdd(&a.stats[2], 1ull);
+    }
+    return;
+  }
+  const int T = a.table_size, mask = T - 1;
+  int* s_key = smem;                 // [T]
+  int* s_val = s_key + T;            // [T] first entry index, later the slot
+  int* s_vic = s_val + T;            // [top_k] victim slot of miss rank r
+  int* s_wave = s_vic + a.top_k;     // [kPlanWaves]
+  int* s_flag = s_wave + kPlanWaves; // [1] host-row error
+  int64_t* tok = a.tokens + req * (int64_t)buf;
+  int64_t* lru = a.lru + req * (int64_t)buf;
+  for (int h = tid; h < T; h += kPlanThreads) {
+    s_key[h] = kEmpty;
+    s_val[h] = 0x7FFFFFFF;
+  }
+  if (tid == 0) *s_flag = 0;
+  __syncthreads();
+
+  // entries i = tid + k*1024 (k < kMaxPerThread)
+  int my_p[kMaxPerThread], my_h[kMaxPerThread];
+  bool my_new[kMaxPerThread];
+  const int64_t newest_pos = s - 1;
+#pragma unroll
+  for (int k = 0; k < kMaxPerThread; ++k) {
+    const int i = tid + k * kPlanThreads;
+    my_p[k] = -1;
+    my_h[k] = -1;
+    my_new[k] = false;
+    if (i < n) {
+      const int p = pos[i];
+      my_p[k] = p;
+      my_new[k] = (int64_t)p == newest_pos;
+      if (!my_new[k]) {  // insert, keep the smallest entry index (first occurrence)
+        uint32_t h = slot_hash(p, mask);
+        for (int probe = 0; probe <= mask; ++probe) {
+          const int old = atomicCAS(&s_key[h], kEmpty, p);
+          if (old == kEmpty || old == p) {
+            atomicMin(&s_val[h], i);
+            my_h[k] = (int)h;
+            break;
+          }
+          h = (h + 1) & (uint32_t)mask;
+        }
+      }
+    }
+  }
+  __syncthreads();
+  bool my_first[kMaxPerThread];
+#pragma unroll
+  for (int k = 0; k < kMaxPerThread; ++k) {
+    const int i = tid + k * kPlanThreads;
+    my_first[k] = i < n && !my_new[k] && my_h[k] >= 0 && s_val[my_h[k]] == i;
+  }
+  __syncthreads();
+  for (int h = tid; h < T; h += kPlanThreads) s_val[h] = -1;  // becomes position -> slot
+  __syncthreads();
+
+  // hits: LRU entries j = tid*E + e (contiguous runs, so ranks follow LRU order)
+  const int E = (buf + kPlanThreads - 1) / kPlanThreads;
+  int my_slot[kMaxPerThread];
+  bool my_hit[kMaxPerThread];
+#pragma unroll
+  for (int e = 0; e < kMaxPerThread; ++e) {
+    const int j = tid * E + e;
+    my_slot[e] = -1;
+    my_hit[e] = false;
+    if (e < E && j < buf) {
+      const int slot = (int)lru[j];
+      my_slot[e] = slot;
+      const int64_t t = (slot >= 0 && slot < buf) ? tok[slot] : -1;
+      if (t >= 0 && t < 0x7FFFFFFF) {
+        const int h = table_find(s_key, (int)t, mask);
+        if (h >= 0) {
+          s_val[h] = slot;
+          my_hit[e] = true;
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  // misses: first occurrences without a hit, ranked in entry order (entry i = tid + k*1024
+  // is not contiguous per thread, so rank by a scan per k-round)
+  int uniq_local = 0;
+  int miss_rank[kMaxPerThread];
+  int num_miss = 0;
+#pragma unroll
+  for (int k = 0; k < kMaxPerThread; ++k) {
+    const bool miss = my_first[k] && s_val[my_h[k] >= 0 ? my_h[k] : 0] < 0;
+    uniq_local += my_first[k] ? 1 : 0;
+    int tot;
+    const int r = block_scan(miss ? 1 : 0, s_wave, &tot);
+    miss_rank[k] = miss ? num_miss + r : -1;
+    num_miss += tot;
+  }
+  // evictable (non-hit) and hit ranks in LRU order
+  int ev_local = 0;
+#pragma unroll
+  for (int e = 0; e < kMaxPerThread; ++e)
+    if (e < E && tid * E + e < buf && !my_hit[e]) ++ev_local;
+  int n_ev;
+  const int ev_base = block_scan(ev_local, s_wave, &n_ev);
+  int uniq_total;
+  (void)block_scan(uniq_local, s_wave, &uniq_total);
+  if (num_miss > n_ev) {  // coordinator.py:278-279
+    if (tid == 0) {
+      atomicOr(a.err, kErrVictims);
+      a.copy_count[b] = 0;
+    }
+    for (int i = tid; i < a.top_k; i += kPlanThreads) rows[i] = -1;
+    return;
+  }
+  {
+    int e_rank = ev_base;
+#pragma unroll
+    for (int e = 0; e < kMaxPerThread; ++e) {
+      if (e < E && tid * E + e < buf && !my_hit[e]) {
+        if (e_rank < num_miss) s_vic[e_rank] = my_slot[e];
+        ++e_rank;
+      }
+    }
+  }
+  __syncthreads();
+  // victims: host rows must exist (coordinator.py:284-286), then record the copies
+  int64_t* cdst = a.copy_dst + (int64_t)b * a.top_k;
+  int64_t* csrc = a.copy_src + (int64_t)b * a.top_k;
+#pragma unroll
+  for (int k = 0; k < kMaxPerThread; ++k) {
+    if (miss_rank[k] >= 0) {
+      const int slot = s_vic[miss_rank[k]];
+      const int64_t p = my_p[k];
+      const int64_t host = (p >= 0 && p < a.r2h_stride) ? a.r2h[req * a.r2h_stride + p] : -1;
+      if (host < 0) atomicOr(s_flag, 1);
+      s_val[my_h[k]] = slot;
+      cdst[miss_rank[k]] = base_row + slot;
+      csrc[miss_rank[k]] = host;
+    }
+  }
+  __syncthreads();
+  if (*s_flag) {
+    if (tid == 0) {
+      atomicOr(a.err, kErrHostRow);
+      a.copy_count[b] = 0;
+    }
+    for (int i = tid; i < a.top_k; i += kPlanThreads) rows[i] = -1;
+    return;
+  }
+  // commit: tokens of the victims, new LRU order (coordinator.py:291, 295)
+#pragma unroll
+  for (int k = 0; k < kMaxPerThread; ++k)
+    if (miss_rank[k] >= 0) tok[s_vic[miss_rank[k]]] = my_p[k];
+  {
+    int e_rank = ev_base, h_rank = min(tid * E, buf) - ev_base;  // hits before this thread's run
+#pragma unroll
+    for (int e = 0; e < kMaxPerThread; ++e) {
+      if (e < E && tid * E + e < buf) {
+        int dst;
+        if (!my_hit[e]) {
+          dst = e_rank >= num_miss ? e_rank - num_miss : (n_ev - num_miss) + e_rank;
+          ++e_rank;
+        } else {
+          dst = n_ev + h_rank;
+          ++h_rank;
+        }
+        lru[dst] = my_slot[e];
+      }
+    }
+  }
+  // rows of every entry, duplicates included (coordinator.py:298-300)
+#pragma unroll
+  for (int k = 0; k < kMaxPerThread; ++k) {
+    const int i = tid + k * kPlanThreads;
+    if (i < n) rows[i] = my_new[k] ? base_row + buf : base_row + s_val[my_h[k]];
+  }
+  for (int i = n + tid; i < a.top_k; i += kPlanThreads) rows[i] = -1;
+  if (tid == 0) {
+    a.copy_count[b] = num_miss;
+    atomicAdd(&a.stats[0], (unsigned long long)(uniq_total - num_miss));
+    atomicAdd(&a.stats[1], (unsigned long long)num_miss);
+  }
+}
+
+// Host -> device rows of the planned misses: grid (top_k / 4, bs), 64 threads per row.
+__global__ __launch_bounds__(256) void swap_copy_kernel(const int64_t* copy_dst, const int64_t* copy_src,
+                                                       const int32_t* copy_count, int top_k,
+                                                       char* dev_k, char* dev_v, const char* host_k,
+                                                       const char* host_v, int64_t row_bytes,
+                                                       int64_t dev_rows, int64_t host_rows) {
+  const int b = blockIdx.y;
+  const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= copy_count[b]) return;
+  const int64_t dst = copy_dst[(int64_t)b * top_k + r];
+  const int64_t src = copy_src[(int64_t)b * top_k + r];
+  if (dst < 0 || dst >= dev_rows || src < 0 || src >= host_rows) return;
+  const int lane = threadIdx.x & 63;
+  const int64_t units = row_bytes / 16;
+  const uint4* hk = reinterpret_cast<const uint4*>(host_k + src * row_bytes);
+  const uint4* hv = reinterpret_cast<const uint4*>(host_v + src * row_bytes);
+  uint4* dk = reinterpret_cast<uint4*>(dev_k + dst * row_bytes);
+  uint4* dv = reinterpret_cast<uint4*>(dev_v + dst * row_bytes);
+  for (int64_t u = lane; u < units; u += 64) {
+    const uint4 x = hk[u];
+    const uint4 y = hv[u];
+    dk[u] = x;
+    dv[u] = y;
+  }
+}
+
+// Row copies for every layer: dst[layer][dst_row(i)] = src[layer][src_row(i)].
+// Rows whose index falls outside its buffer are skipped.
+__global__ __launch_bounds__(256) void copy_rows_kernel(const char* src, int64_t src_layer_stride,
+                                                       int64_t src_rows, const int64_t* src_idx,
+                                                       char* dst, int64_t dst_layer_stride,
+                                                       int64_t dst_rows, const int64_t* dst_idx,
+                                                       int64_t row_bytes) {
+  const int i = blockIdx.x, layer = blockIdx.y;
+  const int64_t s = src_idx[i], d = dst_idx[i];
+  if (s < 0 || s >= src_rows || d < 0 || d >= dst_rows) return;
+  const uint4* sp = reinterpret_cast<const uint4*>(src + layer * src_layer_stride + s * row_bytes);
+  uint4* dp = reinterpret_cast<uint4*>(dst + layer * dst_layer_stride + d * row_bytes);
+  for (int64_t u = threadIdx.x; u < row_bytes / 16; u += 256) dp[u] = sp[u];
+}
+
+// Per-request bookkeeping: mode 0 = admit (tokens[s] = s, lru[s] = s, host rows of
+// positions [0, n)), mode 1 = release (tokens = -1, lru[s] = s, host rows = -1).
+__global__ __launch_bounds__(256) void request_state_kernel(int64_t* tokens, int64_t* lru, int L, int R,
+                                                          int buf, int64_t* r2h, int64_t r2h_stride,
+                                                          int req, const int64_t* host_idx, int64_t n,
+                                                          int mode) {
+  const int layer = blockIdx.y;
+  const int64_t off = ((int64_t)layer * R + req) * buf;
+  for (int s = blockIdx.x * 256 + threadIdx.x; s < buf; s += gridDim.x * 256) {
+    tokens[off + s] = mode == 0 ? (int64_t)s : -1;
+    lru[off + s] = s;
+  }
+  if (layer == 0) {
+    int64_t* row = r2h + (int64_t)req * r2h_stride;
+    for (int64_t p = blockIdx.x * 256 + threadIdx.x; p < r2h_stride; p += gridDim.x * 256)
+      row[p] = (mode == 0 && p < n) ? host_idx[p] : -1;
+  }
+}
+
+// Eager backup bookkeeping (coordinator.py:201-212): for listed request i (prev
+// position seq-2, skipped when the flag is set), the device row of the previous
+// token and req_to_host_pool[req, seq-2] = host_idx[i].
+__global__ __launch_bounds__(256) void backup_index_kernel(const int64_t* reqs, const int64_t* seq,
+                                                         const int64_t* host_idx, int n, int buf,
+                                                         int R, int64_t* r2h, int64_t r2h_stride,
+                                                         int64_t* dev_rows) {
+  for (int i = threadIdx.x; i < n; i += 256) {
+    const int64_t req = reqs[i];
+    const int64_t prev = seq[i] - 2;
+    if (req < 0 || req >= R || prev < 0 || prev >= r2h_stride) {
+      dev_rows[i] = -1;
+      continue;
+    }
+    dev_rows[i] = req * (int64_t)(buf + 1) + min(prev, (int64_t)buf);
+    r2h[req * r2h_stride + prev] = host_idx[i];
+  }
+}
+
+// write_new_token (coordinator.py:217-228): slot min(seq-1, buf) of each request.
+template <typename Dst, typename Src>
+__global__ __launch_bounds__(256) void write_new_kernel(Dst* k_dst, Dst* v_dst, const Src* k_src,
+                                                      const Src* v_src, const int64_t* rpi,
+                                                      const int64_t* seq, int buf, int R,
+                                                      int64_t row_elems) {
+  const int b = blockIdx.x;
+  const int64_t req = rpi[b];
+  if (req < 0 || req >= R) return;
+  const int64_t loc = req * (int64_t)(buf + 1) + min(seq[b] - 1, (int64_t)buf);
+  for (int64_t e = threadIdx.x; e < row_elems; e += 256) {
+    if constexpr (sizeof(Dst) == sizeof(Src)) {
+      k_dst[loc * row_elems + e] = k_src[(int64_t)b * row_elems + e];
+      v_dst[loc * row_elems + e] = v_src[(int64_t)b * row_elems + e];
+    } else if constexpr (sizeof(Dst) == 2) {
+      k_dst[loc * row_elems + e] = f2bf((float)k_src[(int64_t)b * row_elems + e]);
+      v_dst[loc * row_elems + e] = f2bf((float)v_src[(int64_t)b * row_elems + e]);
+    } else {
+      k_dst[loc * row_elems + e] = bf2f(k_src[(int64_t)b * row_elems + e]);
+      v_dst[loc * row_elems + e] = bf2f(v_src[(int64_t)b * row_elems + e]);
+    }
+  }
+}
+
+}  // namespace
+}  // namespace qq
+
+using namespace qq;
+
+extern "C" int qq_hisparse_swap_in(const int32_t* positions, int64_t positions_stride,
+                                   const int32_t* actual_lens, const int64_t* seq_lens,
+                                   const int64_t* req_pool_indices, int bs, int max_reqs,
+                                   int device_buffer_size, int top_k, int64_t* buffer_tokens_layer,
+                                   int64_t* lru_slots_layer, const int64_t* req_to_host_pool,
+                                   int64_t max_context_len, void* device_k_layer,
+                                   void* device_v_layer, const void* host_k_layer,
+                                   const void* host_v_layer, int64_t row_bytes,
+                                   int64_t host_rows, int64_t* rows_out, int64_t* copy_dst,
+                                   int64_t* copy_src, int32_t* copy_count, uint64_t* stats,
+                                   int32_t* error_flags, void* stream) {
+  const char* what = "qq_hisparse_swap_in";
+  QQ_REQUIRE(bs >= 0 && max_reqs > 0 && device_buffer_size >= top_k && top_k > 0,
+             "%s: bad sizes (buf %d, top_k %d)", what, device_buffer_size, top_k);
+  QQ_REQUIRE(device_buffer_size <= kMaxPerThread * kPlanThreads && top_k <= kMaxPerThread * kPlanThreads,
+             "%s: buffer %d / top_k %d exceed %d", what, device_buffer_size, top_k,
+             kMaxPerThread * kPlanThreads);
+  QQ_REQUIRE(row_bytes > 0 && row_bytes % 16 == 0, "%s: row bytes %lld must be a multiple of 16",
+             what, (long long)row_bytes);
+  QQ_REQUIRE(positions_stride >= top_k, "%s: positions stride < top_k", what);
+  if (bs == 0) return QQ_OK;
+  int T = 1;
+  while (T < 2 * top_k) T <<= 1;
+  const size_t smem = (size_t)(2 * T + top_k + kPlanWaves + 1) * sizeof(int);
+  QQ_REQUIRE(smem <= 64 * 1024, "%s: top_k %d needs %zu bytes of LDS", what, top_k, smem);
+  SwapArgs a;
+  a.positions = positions;
+  a.pos_stride = positions_stride;
+  a.actual = actual_lens;
+  a.seq = seq_lens;
+  a.rpi = req_pool_indices;
+  a.tokens = buffer_tokens_layer;
+  a.lru = lru_slots_layer;
+  a.r2h = req_to_host_pool;
+  a.r2h_stride = max_context_len;
+  a.R = max_reqs;
+  a.buf = device_buffer_size;
+  a.top_k = top_k;
+  a.rows_out = rows_out;
+  a.rows_stride = top_k;
+  a.copy_dst = copy_dst;
+  a.copy_src = copy_src;
+  a.copy_count = copy_count;
+  a.stats = reinterpret_cast<unsigned long long*>(stats);
+  a.err = error_flags;
+  a.table_size = T;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  swap_plan_kernel<<<bs, kPlanThreads, smem, s>>>(a);
+  swap_copy_kernel<<<dim3((top_k + 3) / 4, bs), 256, 0, s>>>(
+      copy_dst, copy_src, copy_count, top_k, static_cast<char*>(device_k_layer),
+      static_cast<char*>(device_v_layer), static_cast<const char*>(host_k_layer),
+      static_cast<const char*>(host_v_layer), row_bytes,
+      (int64_t)max_reqs * (device_buffer_size + 1), host_rows);
+  return check_launch(what);
+}
+
+extern "C" int qq_copy_rows(const void* src, int64_t src_layer_stride_bytes, int64_t src_rows,
+                            const int64_t* src_idx, void* dst, int64_t dst_layer_stride_bytes,
+                            int64_t dst_rows, const int64_t* dst_idx, int n, int n_layers,
+                            int64_t row_bytes, void* stream) {
+  QQ_REQUIRE(n >= 0 && n_layers > 0 && row_bytes > 0 && row_bytes % 16 == 0,
+             "qq_copy_rows: bad sizes");
+  if (n == 0) return QQ_OK;
+  copy_rows_kernel<<<dim3(n, n_layers), 256, 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<const char*>(src), src_layer_stride_bytes, src_rows, src_idx,
+      static_cast<char*>(dst), dst_layer_stride_bytes, dst_rows, dst_idx, row_bytes);
+  return check_launch("qq_copy_rows");
+}
+
+extern "C" int qq_hisparse_request_state(int64_t* buffer_tokens, int64_t* lru_slots, int num_layers,
+                                         int max_reqs, int device_buffer_size,
+                                         int64_t* req_to_host_pool, int64_t max_context_len,
+                                         int req, const int64_t* host_idx, int64_t n, int release,
+                                         void* stream) {
+  QQ_REQUIRE(req >= 0 && req < max_reqs && num_layers > 0 && device_buffer_size > 0,
+             "qq_hisparse_request_state: bad arguments");
+  QQ_REQUIRE(release || n == 0 || host_idx, "qq_hisparse_request_state: host rows missing");
+  QQ_REQUIRE(n <= max_context_len, "qq_hisparse_request_state: %lld positions exceed %lld",
+             (long long)n, (long long)max_context_len);
+  const int blocks = max(1, min(ceil_div(max((int64_t)device_buffer_size, max_context_len), 256), 512));
+  request_state_kernel<<<dim3(blocks, num_layers), 256, 0, static_cast<hipStream_t>(stream)>>>(
+      buffer_tokens, lru_slots, num_layers, max_reqs, device_buffer_size, req_to_host_pool,
+      max_context_len, req, host_idx, n, release ? 1 : 0);
+  return check_launch("qq_hisparse_request_state");
+}
+
+extern "C" int qq_hisparse_backup_index(const int64_t* req_indices, const int64_t* seq_lens,
+                                        const int64_t* host_idx, int n, int device_buffer_size,
+                                        int max_reqs, int64_t* req_to_host_pool,
+                                        int64_t max_context_len, int64_t* device_rows,
+                                        void* stream) {
+  QQ_REQUIRE(n >= 0 && device_buffer_size > 0, "qq_hisparse_backup_index: bad arguments");
+  if (n == 0) return QQ_OK;
+  backup_index_kernel<<<1, 256, 0, static_cast<hipStream_t>(stream)>>>(
+      req_indices, seq_lens, host_idx, n, device_buffer_size, max_reqs, req_to_host_pool,
+      max_context_len, device_rows);
+  return check_launch("qq_hisparse_backup_index");
+}
+
+extern "C" int qq_hisparse_write_new_token(void* device_k_layer, void* device_v_layer,
+                                           int buf_dtype, const void* k, const void* v,
+                                           int src_dtype, const int64_t* req_pool_indices,
+                                           const int64_t* seq_lens, int bs,
+                                           int device_buffer_size, int max_reqs,
+                                           int64_t row_elems, void* stream) {
+  QQ_REQUIRE(dtype_ok(buf_dtype) && dtype_ok(src_dtype), "qq_hisparse_write_new_token: dtype");
+  QQ_REQUIRE(bs >= 0 && row_elems > 0, "qq_hisparse_write_new_token: bad sizes");
+  if (bs == 0) return QQ_OK;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (buf_dtype == QQ_DTYPE_BF16 && src_dtype == QQ_DTYPE_BF16)
+    write_new_kernel<uint16_t, uint16_t><<<bs, 256, 0, s>>>(
+        (uint16_t*)device_k_layer, (uint16_t*)device_v_layer, (const uint16_t*)k,
+        (const uint16_t*)v, req_pool_indices, seq_lens, device_buffer_size, max_reqs, row_elems);
+  else if (buf_dtype == QQ_DTYPE_F32 && src_dtype == QQ_DTYPE_F32)
+    write_new_kernel<float, float><<<bs, 256, 0, s>>>(
+        (float*)device_k_layer, (float*)device_v_layer, (const float*)k, (const float*)v,
+        req_pool_indices, seq_lens, device_buffer_size, max_reqs, row_elems);
+  else if (buf_dtype == QQ_DTYPE_BF16)
+    write_new_kernel<uint16_t, float><<<bs, 256, 0, s>>>(
+        (uint16_t*)device_k_layer, (uint16_t*)device_v_layer, (const float*)k, (const float*)v,
+        req_pool_indices, seq_lens, device_buffer_size, max_reqs, row_elems);
+  else
+    write_new_kernel<float, uint16_t><<<bs, 256, 0, s>>>(
+        (float*)device_k_layer, (float*)device_v_layer, (const uint16_t*)k, (const uint16_t*)v,
+        req_pool_indices, seq_lens, device_buffer_size, max_reqs, row_elems);
+  return check_launch("qq_hisparse_write_new_token");
+}
+
+extern "C" int qq_host_device_pointer(void* host_ptr, void** device_ptr) {
+  QQ_REQUIRE(host_ptr && device_ptr, "qq_host_device_pointer: null pointer");
+  const hipError_t e = hipHostGetDevicePointer(device_ptr, host_ptr, 0);
+  if (e != hipSuccess)
+    return set_error(QQ_EHIP, "hipHostGetDevicePointer: %s (is the memory pinned?)",
+                     hipGetErrorString(e));
+  return QQ_OK;
+}

@@ -1,0 +1,290 @@
+"""HiSparse hierarchical KV cache, Quest mode (reference ``src/qwenquest/hisparse/coordinator.py``).
+
+Two tiers, the reference's layout and bookkeeping:
+
+* host: every request's full KV history in **pinned host memory**
+  (``host_k/v[layer]``, rows handed out by ``host_allocator``), addressed by
+  ``req_to_host_pool[req, position]``;
+* device: per request ``device_buffer_size`` LRU slots + 1 reserved newest-token
+  slot (``device_k/v[layer]``, ``buffer_tokens``, ``lru_slots``).
+
+All copies and the swap-in planning run in HIP kernels on the current stream;
+the kernels read/write the pinned host tier directly over PCIe, so a decode
+step needs no host synchronisation.  The two error conditions of the
+reference's swap-in (too few victims, a position without host backup) are
+raised by :meth:`check_errors`, which :meth:`prepare_decode_step`, ``stats``
+and (with ``sync_errors=True``) every swap-in call run.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import torch
+
+from qwenquest_amd import _lib
+from qwenquest_amd.memory import MHATokenToKVPool, TokenToKVPoolAllocator
+from qwenquest_amd.quest import QuestAlgorithm
+
+__all__ = ["HiSparseCoordinator", "SwapInStats"]
+
+_ERR_VICTIMS, _ERR_HOST_ROW = 1, 2
+
+
+@dataclass
+class SwapInStats:
+    """Hit/miss accounting of the LRU hot buffer (coordinator.py:48-59)."""
+
+    hits: int = 0
+    misses: int = 0
+    fast_path_calls: int = 0
+
+    @property
+    def hit_rate(self) -> float:
+        total = self.hits + self.misses
+        return self.hits / total if total else float("nan")
+
+
+class HiSparseCoordinator:
+    def __init__(
+        self,
+        *,
+        quest: QuestAlgorithm,
+        num_layers: int,
+        kv_heads: int,
+        head_dim: int,
+        max_reqs: int,
+        max_context_len: int,
+        top_k: int,
+        device_buffer_size: int,
+        host_pool_size: int,
+        dtype: torch.dtype,
+        device: torch.device | str,
+        host_device: torch.device | str = "cpu",
+        sync_errors: bool = False,
+    ):
+        # coordinator.py:91-94
+        if device_buffer_size < top_k:
+            raise ValueError("device_buffer_size must be >= top_k")
+        if quest.top_k != top_k:
+            raise ValueError(f"QuestAlgorithm.top_k ({quest.top_k}) != top_k ({top_k})")
+        self.device = torch.device(device)
+        self.host_device = torch.device(host_device)
+        if self.device.type != "cuda":
+            raise RuntimeError("qwenquest_amd.HiSparseCoordinator needs a GPU device (no CPU path)")
+        if self.host_device.type != "cpu":
+            raise ValueError("the host tier lives in pinned CPU memory: host_device must be 'cpu'")
+        self.quest = quest
+        self.num_layers = num_layers
+        self.kv_heads, self.head_dim = kv_heads, head_dim
+        self.max_reqs, self.max_context_len = max_reqs, max_context_len
+        self.top_k = top_k
+        self.device_buffer_size = buf = device_buffer_size
+        self.dtype = dtype
+        self.sync_errors = sync_errors
+        self.row_elems = kv_heads * head_dim
+        self.row_bytes = self.row_elems * torch.tensor([], dtype=dtype).element_size()
+
+        # ---- host tier (pinned), full history of every request
+        self.host_allocator = TokenToKVPoolAllocator(host_pool_size, device="cpu")
+        hshape = (num_layers, host_pool_size + 1, kv_heads, head_dim)
+        self.host_k_all = torch.zeros(hshape, dtype=dtype, pin_memory=True)
+        self.host_v_all = torch.zeros(hshape, dtype=dtype, pin_memory=True)
+        self.host_k = list(self.host_k_all.unbind(0))
+        self.host_v = list(self.host_v_all.unbind(0))
+        self._host_k_dev = self._device_address(self.host_k_all)
+        self._host_v_dev = self._device_address(self.host_v_all)
+        self.req_to_host_pool = torch.full((max_reqs, max_context_len), -1, dtype=torch.int64, device=self.device)
+
+        # ---- device tier: per request buf LRU slots + 1 newest-token slot
+        dshape = (num_layers, max_reqs * (buf + 1), kv_heads, head_dim)
+        self.device_k_all = torch.zeros(dshape, dtype=dtype, device=self.device)
+        self.device_v_all = torch.zeros(dshape, dtype=dtype, device=self.device)
+        self.device_k = list(self.device_k_all.unbind(0))
+        self.device_v = list(self.device_v_all.unbind(0))
+        self.req_to_device_buffer = torch.arange(max_reqs * (buf + 1), dtype=torch.int64,
+                                                 device=self.device).view(max_reqs, buf + 1)
+        self.buffer_tokens = torch.full((num_layers, max_reqs, buf), -1, dtype=torch.int64, device=self.device)
+        self._lru_init = torch.arange(buf, dtype=torch.int64, device=self.device)
+        self.lru_slots = self._lru_init.repeat(num_layers, max_reqs, 1)
+
+        self._skip_first_backup = [False] * max_reqs
+        # swap-in workspaces + device counters (hits, misses, fast path) + error word
+        self._rows = torch.empty((max_reqs, top_k), dtype=torch.int64, device=self.device)
+        self._copy_dst = torch.empty((max_reqs, top_k), dtype=torch.int64, device=self.device)
+        self._copy_src = torch.empty((max_reqs, top_k), dtype=torch.int64, device=self.device)
+        self._copy_count = torch.zeros(max_reqs, dtype=torch.int32, device=self.device)
+        self._stats = torch.zeros(3, dtype=torch.int64, device=self.device)
+        self._err = torch.zeros(1, dtype=torch.int32, device=self.device)
+
+    @staticmethod
+    def _device_address(t: torch.Tensor) -> int:
+        out = ctypes.c_void_p()
+        _lib.call("qq_host_device_pointer", t.data_ptr(), ctypes.byref(out))
+        return int(out.value)
+
+    def _host_layer(self, base: int, layer: int) -> int:
+        return base + layer * (self.host_k_all.shape[1]) * self.row_bytes
+
+    # -------------------------------------------------- errors / stats
+
+    def check_errors(self) -> None:
+        """Raise what the reference raises inside _swap_in_long (coordinator.py:278-279, 285-286)."""
+        err = int(self._err.item())
+        if err:
+            self._err.zero_()
+            if err & _ERR_VICTIMS:
+                raise RuntimeError("device_buffer_size too small for this top-k")
+            raise AssertionError("positions without host backup were selected")
+
+    @property
+    def stats(self) -> SwapInStats:
+        self.check_errors()
+        h, m, f = self._stats.tolist()
+        return SwapInStats(hits=h, misses=m, fast_path_calls=f)
+
+    # -------------------------------------------------- [H1] admission
+
+    def admit_request(
+        self,
+        req_pool_idx: int,
+        prefill_len: int,
+        token_to_kv_pool: MHATokenToKVPool,
+        prefill_indices: torch.Tensor,
+    ) -> None:
+        """[H1] Back up the prefill to host, keep positions [0, buf) hot, build the bounds
+        (coordinator.py:138-174)."""
+        req = int(req_pool_idx)
+        n = int(prefill_len)
+        buf = self.device_buffer_size
+        stream = _lib.stream(self.device)
+        idx = prefill_indices.to(device=self.device, dtype=torch.int64).contiguous()
+        host_idx = self.host_allocator.alloc(n).to(self.device)
+        pool = token_to_kv_pool
+        _lib.call("qq_hisparse_request_state", _lib.ptr(self.buffer_tokens), _lib.ptr(self.lru_slots),
+                  self.num_layers, self.max_reqs, buf, _lib.ptr(self.req_to_host_pool),
+                  self.max_context_len, req, _lib.ptr(host_idx), n, 0, stream)
+        for src_all, host_base in ((pool.k_all, self._host_k_dev), (pool.v_all, self._host_v_dev)):
+            _lib.call("qq_copy_rows", _lib.ptr(src_all), src_all.stride(0) * src_all.element_size(),
+                      src_all.shape[1], _lib.ptr(idx), host_base,
+                      self.host_k_all.stride(0) * self.host_k_all.element_size(), self.host_k_all.shape[1],
+                      _lib.ptr(host_idx), n, self.num_layers, self.row_bytes, stream)
+        n_dev = min(n, buf)
+        dev_rows = self.req_to_device_buffer[req, :n_dev].contiguous()
+        for src_all, dst_all in ((pool.k_all, self.device_k_all), (pool.v_all, self.device_v_all)):
+            _lib.call("qq_copy_rows", _lib.ptr(src_all), src_all.stride(0) * src_all.element_size(),
+                      src_all.shape[1], _lib.ptr(idx), _lib.ptr(dst_all),
+                      dst_all.stride(0) * dst_all.element_size(), dst_all.shape[1], _lib.ptr(dev_rows),
+                      n_dev, self.num_layers, self.row_bytes, stream)
+        self.quest.update_prefill_representations_fused(req, pool.k_all, idx)
+        self._skip_first_backup[req] = True
+
+    # -------------------------------------------------- [H2] per decode step
+
+    def newest_slot(self, seq_lens: torch.Tensor) -> torch.Tensor:
+        return (seq_lens.long() - 1).clamp(max=self.device_buffer_size)
+
+    def prepare_decode_step(self, req_pool_indices: torch.Tensor, seq_lens: torch.Tensor) -> None:
+        """[H2] Fold the previous token into the bounds, back it up to host (coordinator.py:183-215)."""
+        if not self.sync_errors:
+            self.check_errors()
+        reqs = req_pool_indices.tolist()
+        keep = []
+        for i, r in enumerate(reqs):
+            if self._skip_first_backup[r]:
+                self._skip_first_backup[r] = False
+            else:
+                keep.append(i)
+        if not keep:
+            return
+        stream = _lib.stream(self.device)
+        sel = torch.tensor(keep, dtype=torch.int64, device=self.device)
+        breqs = req_pool_indices.to(device=self.device, dtype=torch.int64)[sel].contiguous()
+        bseq = seq_lens.to(device=self.device, dtype=torch.int64)[sel].contiguous()
+        host_idx = self.host_allocator.alloc(len(keep)).to(self.device)
+        dev_rows = torch.empty(len(keep), dtype=torch.int64, device=self.device)
+        _lib.call("qq_hisparse_backup_index", _lib.ptr(breqs), _lib.ptr(bseq), _lib.ptr(host_idx), len(keep),
+                  self.device_buffer_size, self.max_reqs, _lib.ptr(self.req_to_host_pool),
+                  self.max_context_len, _lib.ptr(dev_rows), stream)
+        self.quest.update_decode_representations_fused(breqs, self.device_k_all, dev_rows)
+        for src_all, host_base in ((self.device_k_all, self._host_k_dev), (self.device_v_all, self._host_v_dev)):
+            _lib.call("qq_copy_rows", _lib.ptr(src_all), src_all.stride(0) * src_all.element_size(),
+                      src_all.shape[1], _lib.ptr(dev_rows), host_base,
+                      self.host_k_all.stride(0) * self.host_k_all.element_size(), self.host_k_all.shape[1],
+                      _lib.ptr(host_idx), len(keep), self.num_layers, self.row_bytes, stream)
+
+    def write_new_token(self, layer_id: int, req_pool_indices: torch.Tensor, seq_lens: torch.Tensor,
+                        k: torch.Tensor, v: torch.Tensor) -> None:
+        """set_kv_buffer redirected into the hot buffer's newest slot (coordinator.py:217-228)."""
+        bs = int(req_pool_indices.shape[0])
+        rpi = req_pool_indices.to(device=self.device, dtype=torch.int64).contiguous()
+        seq = seq_lens.to(device=self.device, dtype=torch.int64).contiguous()
+        kk = k.reshape(bs, self.row_elems).contiguous()
+        vv = v.reshape(bs, self.row_elems).to(kk.dtype).contiguous()
+        _lib.call("qq_hisparse_write_new_token", _lib.ptr(self.device_k[layer_id]),
+                  _lib.ptr(self.device_v[layer_id]), _lib.dtype_code(self.dtype), _lib.ptr(kk), _lib.ptr(vv),
+                  _lib.dtype_code(kk.dtype), _lib.ptr(rpi), _lib.ptr(seq), bs, self.device_buffer_size,
+                  self.max_reqs, self.row_elems, _lib.stream(self.device))
+
+    # -------------------------------------------------- [H3] swap-in
+
+    def swap_in_selected_pages(
+        self,
+        req_pool_indices: torch.Tensor,
+        seq_lens: torch.Tensor,
+        top_k_result: torch.Tensor,
+        layer_id: int,
+        *,
+        actual_lens: torch.Tensor | None = None,
+        out: torch.Tensor | None = None,
+    ) -> torch.Tensor:
+        """[H3] Make the selected positions device-resident; ``[bs, top_k]`` int64 rows of
+        ``device_k/v[layer_id]``, -1 past each request's ``min(seq_len, top_k)``
+        (coordinator.py:232-304)."""
+        bs = int(req_pool_indices.shape[0])
+        if bs > self.max_reqs:
+            raise ValueError(f"batch {bs} exceeds max_reqs {self.max_reqs}")
+        rpi = req_pool_indices.to(device=self.device, dtype=torch.int64).contiguous()
+        seq = seq_lens.to(device=self.device, dtype=torch.int64).contiguous()
+        pos = top_k_result.to(device=self.device, dtype=torch.int32)
+        if pos.shape[1] < self.top_k:
+            pos = torch.nn.functional.pad(pos, (0, self.top_k - pos.shape[1]))
+        pos = pos.contiguous()
+        actual = actual_lens if actual_lens is not None else seq.clamp(max=self.top_k).to(torch.int32)
+        actual = actual.to(device=self.device, dtype=torch.int32).contiguous()
+        rows = out if out is not None else torch.empty((bs, self.top_k), dtype=torch.int64, device=self.device)
+        _lib.call(
+            "qq_hisparse_swap_in", _lib.ptr(pos), pos.stride(0), _lib.ptr(actual), _lib.ptr(seq), _lib.ptr(rpi),
+            bs, self.max_reqs, self.device_buffer_size, self.top_k, _lib.ptr(self.buffer_tokens[layer_id]),
+            _lib.ptr(self.lru_slots[layer_id]), _lib.ptr(self.req_to_host_pool), self.max_context_len,
+            _lib.ptr(self.device_k[layer_id]), _lib.ptr(self.device_v[layer_id]),
+            self._host_layer(self._host_k_dev, layer_id), self._host_layer(self._host_v_dev, layer_id),
+            self.row_bytes, self.host_k_all.shape[1], _lib.ptr(rows), _lib.ptr(self._copy_dst),
+            _lib.ptr(self._copy_src), _lib.ptr(self._copy_count), _lib.ptr(self._stats), _lib.ptr(self._err),
+            _lib.stream(self.device),
+        )
+        if self.sync_errors:
+            self.check_errors()
+        return rows
+
+    # -------------------------------------------------- [H4] release
+
+    def request_finished(self, req_pool_idx: int) -> None:
+        """[H4] Free the host rows, reset the request's state and bounds (coordinator.py:308-316)."""
+        req = int(req_pool_idx)
+        host_idx = self.req_to_host_pool[req].cpu()
+        self.host_allocator.free(host_idx[host_idx >= 0])
+        _lib.call("qq_hisparse_request_state", _lib.ptr(self.buffer_tokens), _lib.ptr(self.lru_slots),
+                  self.num_layers, self.max_reqs, self.device_buffer_size, _lib.ptr(self.req_to_host_pool),
+                  self.max_context_len, req, None, 0, 1, _lib.stream(self.device))
+        self._skip_first_backup[req] = False
+        self.quest.invalidate_request(req)
+
+    # -------------------------------------------------- introspection
+
+    def device_bytes(self) -> int:
+        return 2 * self.device_k_all.numel() * self.device_k_all.element_size()
+
+    def host_bytes(self) -> int:
+        return 2 * self.host_k_all.numel() * self.host_k_all.element_size()

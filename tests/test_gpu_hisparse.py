@@ -1,0 +1,270 @@
+"""GPU parity of the HiSparse hot buffer: exactness of the swap-in, the LRU state
+machine (known answers + the reference's 200-step golden trace), eager backup,
+release, error conditions, and quest_hisparse == quest bit for bit."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import hisparse as oh
+from tests.conftest import load_golden
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda", 0)
+LAYERS, KV, D = 2, 2, 8
+
+
+def make(buf: int, top_k: int, page: int = 1, max_reqs: int = 2, max_ctx: int = 256, dtype=torch.float32):
+    from qwenquest_amd.hisparse import HiSparseCoordinator
+    from qwenquest_amd.memory import MHATokenToKVPool
+    from qwenquest_amd.quest import QuestAlgorithm
+
+    quest = QuestAlgorithm(top_k=top_k, page_size=page, device=DEV)
+    quest.init_storage(0, LAYERS, max_reqs, max_ctx, KV, D)
+    coord = HiSparseCoordinator(
+        quest=quest, num_layers=LAYERS, kv_heads=KV, head_dim=D, max_reqs=max_reqs,
+        max_context_len=max_ctx, top_k=top_k, device_buffer_size=buf,
+        host_pool_size=max_reqs * max_ctx, dtype=dtype, device=DEV,
+    )
+    pool = MHATokenToKVPool(max_ctx, LAYERS, KV, D, dtype, DEV)
+    return quest, coord, pool
+
+
+def truth(total: int, seed: int = 0):
+    gen = torch.Generator().manual_seed(seed)
+    return torch.randn(LAYERS, total, KV, D, generator=gen), torch.randn(LAYERS, total, KV, D, generator=gen)
+
+
+def admit(coord, pool, req, n, k, v):
+    locs = torch.arange(1, n + 1, device=DEV)
+    for layer in range(LAYERS):
+        pool.set_kv_buffer(layer, locs, k[layer, :n].to(DEV), v[layer, :n].to(DEV))
+    coord.admit_request(req, n, pool, locs)
+
+
+def decode_step(coord, req, pos, k, v):
+    reqs, seq_lens = torch.tensor([req], device=DEV), torch.tensor([pos + 1], device=DEV)
+    coord.prepare_decode_step(reqs, seq_lens)
+    for layer in range(LAYERS):
+        coord.write_new_token(layer, reqs, seq_lens, k[layer, pos : pos + 1].to(DEV), v[layer, pos : pos + 1].to(DEV))
+    return reqs, seq_lens
+
+
+@pytest.mark.parametrize(("prefill_len", "buf", "top_k"), [(10, 16, 8), (40, 16, 8), (5, 32, 32)])
+def test_swap_in_is_exact_under_random_selections(prefill_len, buf, top_k):
+    """reference tests/test_hisparse.py:65-90, plus the oracle's rows and LRU state each step."""
+    total = 120
+    k, v = truth(total)
+    _, coord, pool = make(buf, top_k)
+    admit(coord, pool, 1, prefill_len, k, v)
+    st = oh.HiSparseState(LAYERS, 2, buf=buf, top_k=top_k, max_ctx=256)
+    st.admit(1, np.arange(prefill_len))
+    gen = torch.Generator().manual_seed(7)
+    for pos in range(prefill_len, total):
+        reqs, seq_lens = decode_step(coord, 1, pos, k, v)
+        if pos > prefill_len:
+            st.backup(1, pos - 1, pos - 1)
+        seq_len = pos + 1
+        n = min(seq_len, top_k)
+        for layer in range(LAYERS):
+            if seq_len <= top_k:
+                sel = torch.arange(n)
+            else:
+                sel = torch.randint(0, seq_len, (n,), generator=gen)
+                sel[-1] = seq_len - 1
+                sel[0] = sel[1]
+            rows = coord.swap_in_selected_pages(reqs, seq_lens, sel[None].int(), layer)
+            got_k = coord.device_k[layer][rows[0, :n]].cpu()
+            got_v = coord.device_v[layer][rows[0, :n]].cpu()
+            assert torch.equal(got_k, k[layer, sel]), f"layer {layer} pos {pos}"
+            assert torch.equal(got_v, v[layer, sel])
+            ref_rows, _ = st.swap_in(layer, [1], [seq_len], sel[None].numpy())
+            assert np.array_equal(rows.cpu().numpy()[0, :n], ref_rows[0, :n])
+            assert np.array_equal(coord.buffer_tokens[layer, 1].cpu().numpy(), st.buffer_tokens[layer, 1])
+            assert np.array_equal(coord.lru_slots[layer, 1].cpu().numpy(), st.lru_slots[layer, 1])
+            if seq_len > top_k:
+                assert rows[0, 0] == rows[0, 1]
+    stats = coord.stats
+    assert stats.misses > 0 and (stats.hits, stats.misses) == (st.hits, st.misses)
+
+
+def test_every_decoded_token_is_backed_up_to_host():
+    k, v = truth(64)
+    _, coord, pool = make(buf=8, top_k=8)
+    admit(coord, pool, 0, 20, k, v)
+    for pos in range(20, 41):
+        decode_step(coord, 0, pos, k, v)
+    torch.cuda.synchronize()
+    host_idx = coord.req_to_host_pool[0, :40].cpu()
+    assert torch.all(host_idx >= 0)
+    for layer in range(LAYERS):
+        assert torch.equal(coord.host_k[layer][host_idx], k[layer, :40])
+        assert torch.equal(coord.host_v[layer][host_idx], v[layer, :40])
+    assert int(coord.req_to_host_pool[0, 40]) == -1
+
+
+def test_lru_replacement_order_known_answer():
+    """reference tests/test_hisparse.py:108-129."""
+    k, v = truth(32)
+    _, coord, pool = make(buf=4, top_k=2)
+    admit(coord, pool, 0, 10, k, v)
+
+    def select(pos, positions):
+        reqs, seq_lens = decode_step(coord, 0, pos, k, v)
+        coord.swap_in_selected_pages(reqs, seq_lens, torch.tensor([positions]).int(), 0)
+
+    select(10, [5, 10])
+    assert coord.buffer_tokens[0, 0].tolist() == [5, 1, 2, 3]
+    assert coord.lru_slots[0, 0].tolist() == [1, 2, 3, 0]
+    select(11, [1, 5])
+    assert (coord.stats.hits, coord.stats.misses) == (2, 1)
+    assert coord.lru_slots[0, 0].tolist() == [2, 3, 1, 0]
+    select(12, [7, 8])
+    assert coord.buffer_tokens[0, 0].tolist() == [5, 1, 7, 8]
+    assert coord.lru_slots[0, 0].tolist() == [1, 0, 2, 3]
+    assert (coord.stats.hits, coord.stats.misses) == (2, 3)
+
+
+def test_fast_path_while_sequence_fits_the_buffer():
+    k, v = truth(32)
+    _, coord, pool = make(buf=16, top_k=16)
+    admit(coord, pool, 0, 6, k, v)
+    reqs, seq_lens = decode_step(coord, 0, 6, k, v)
+    rows = coord.swap_in_selected_pages(reqs, seq_lens, torch.arange(16)[None].int(), 0)
+    assert rows[0, :7].tolist() == coord.req_to_device_buffer[0, :7].tolist()
+    assert torch.all(rows[0, 7:] == -1)
+    assert coord.stats.fast_path_calls == 1 and coord.stats.misses == 0
+
+
+def test_request_finished_releases_everything():
+    k, v = truth(64)
+    quest, coord, pool = make(buf=8, top_k=8, page=4)
+    free_before = coord.host_allocator.available_size()
+    admit(coord, pool, 1, 30, k, v)
+    for pos in range(30, 36):
+        decode_step(coord, 1, pos, k, v)
+    assert quest.page_valid[:, 1].any()
+    coord.request_finished(1)
+    assert coord.host_allocator.available_size() == free_before
+    assert torch.all(coord.req_to_host_pool[1] == -1)
+    assert torch.all(coord.buffer_tokens[:, 1] == -1)
+    assert not quest.page_valid[:, 1].any()
+
+
+def test_coordinator_validates_sizes():
+    from qwenquest_amd.hisparse import HiSparseCoordinator
+    from qwenquest_amd.quest import QuestAlgorithm
+
+    quest = QuestAlgorithm(top_k=8, page_size=4, device=DEV)
+    quest.init_storage(0, LAYERS, 1, 64, KV, D)
+    common = dict(quest=quest, num_layers=LAYERS, kv_heads=KV, head_dim=D, max_reqs=1, max_context_len=64,
+                  host_pool_size=64, dtype=torch.float32, device=DEV)
+    with pytest.raises(ValueError):
+        HiSparseCoordinator(top_k=8, device_buffer_size=4, **common)
+    with pytest.raises(ValueError):
+        HiSparseCoordinator(top_k=16, device_buffer_size=32, **common)
+
+
+def test_error_conditions_are_raised():
+    k, v = truth(64)
+    _, coord, pool = make(buf=4, top_k=4)
+    admit(coord, pool, 0, 10, k, v)
+    reqs, seq_lens = decode_step(coord, 0, 10, k, v)
+    # all wanted positions are backed up; 5 distinct misses cannot fit 4 slots... top_k=4 -> 3 + newest
+    tokens_before = coord.buffer_tokens[0, 0].clone()
+    # a position without host backup: position 30 was never decoded
+    coord.req_to_host_pool[0, 9] = -1
+    coord.swap_in_selected_pages(reqs, seq_lens, torch.tensor([[9, 6, 5, 10]]).int(), 0)
+    with pytest.raises(AssertionError):
+        coord.check_errors()
+    assert torch.equal(coord.buffer_tokens[0, 0], tokens_before)  # state left unchanged
+
+
+def test_golden_200_step_trace_through_the_kernels():
+    """The reference's own 200-step trace (tests/golden/swap_trace.npz): identical rows,
+    buffer_tokens, lru_slots and hit/miss counts at every layer of every step."""
+    g = load_golden("swap_trace.npz")
+    layers, buf, top_k, ctx, prefill = g["meta"].tolist()
+    assert layers == LAYERS
+    _, coord, pool = make(buf=buf, top_k=top_k, max_reqs=1, max_ctx=ctx)
+    k, v = truth(ctx, seed=11)
+    admit(coord, pool, 0, prefill, k, v)
+    i = 0
+    for step in range(200):
+        pos = prefill + step
+        reqs, seq_lens = decode_step(coord, 0, pos, k, v)
+        for layer in range(layers):
+            sel = torch.from_numpy(g["selections"][i])
+            rows = coord.swap_in_selected_pages(reqs, seq_lens, sel[None].int(), layer)
+            assert np.array_equal(rows[0].cpu().numpy(), g["rows"][i]), f"step {step} layer {layer}"
+            assert np.array_equal(coord.buffer_tokens[layer, 0].cpu().numpy(), g["tokens"][i])
+            assert np.array_equal(coord.lru_slots[layer, 0].cpu().numpy(), g["lru"][i])
+            assert torch.equal(coord.device_k[layer][rows[0]].cpu(), k[layer, sel])
+            i += 1
+    s = coord.stats
+    assert [s.hits, s.misses] == g["stats"][-1].tolist()
+
+
+@pytest.mark.parametrize("avoid", [False, True])
+def test_quest_hisparse_is_bit_identical_to_quest(avoid):
+    """reference tests/test_engine.py:59-69 and test_bf16.py:27-43 at the backend boundary:
+    the same q/k/v through QuestOnlyBackend and QuestHiSparseBackend over many decode steps
+    (the hot buffer must swap) give bit-identical outputs."""
+    from qwenquest_amd.attention.quest_hisparse import QuestHiSparseBackend
+    from qwenquest_amd.attention.quest_only import QuestOnlyBackend
+    from qwenquest_amd.batch import ForwardBatch, ForwardMode
+    from qwenquest_amd.memory import MHATokenToKVPool, ReqToTokenPool
+
+    L, H, KVH, DIM, CTX = 3, 8, 2, 16, 256
+    cfg = {"algorithm": "quest", "top_k": 32, "quest_page_size": 8, "device_buffer_size": 48,
+           "avoid_recent_overlap": avoid}
+    gen = torch.Generator().manual_seed(3)
+    prompts = {0: 90, 1: 107}
+    steps = 60
+    total = max(prompts.values()) + steps + 1
+    kk = torch.randn(L, 2, total, KVH, DIM, generator=gen).to(torch.bfloat16)
+    vv = torch.randn(L, 2, total, KVH, DIM, generator=gen).to(torch.bfloat16)
+    qq = torch.randn(steps, L, 2, H, DIM, generator=gen).to(torch.bfloat16)
+    outs = {}
+    for mode in ("quest", "quest_hisparse"):
+        rtp = ReqToTokenPool(2, CTX, DEV)
+        kvp = MHATokenToKVPool(2 * CTX, L, KVH, DIM, torch.bfloat16, DEV)
+        if mode == "quest":
+            be = QuestOnlyBackend(rtp, kvp, cfg)
+        else:
+            be = QuestHiSparseBackend(rtp, kvp, cfg, host_pool_size=2 * CTX)
+        for r, n in prompts.items():
+            rtp.req_to_token[r] = torch.arange(1 + r * CTX, 1 + (r + 1) * CTX, dtype=torch.int32)
+            rows = torch.arange(1 + r * CTX, 1 + r * CTX + n)
+            kvp.k_all[:, rows] = kk[:, r, :n].to(DEV)
+            kvp.v_all[:, rows] = vv[:, r, :n].to(DEV)
+        batch = ForwardBatch(ForwardMode.EXTEND, None, None, torch.tensor([0, 1]), torch.tensor(list(prompts.values())),
+                             None, rtp, kvp, be)
+        if mode == "quest":
+            be._update_quest_for_extend(batch)
+        else:
+            be.on_extend_finished(batch)
+
+        class Layer:
+            def __init__(self, i):
+                self.layer_id, self.scaling = i, DIM**-0.5
+
+        res = []
+        for step in range(steps):
+            seqs = [prompts[r] + step + 1 for r in (0, 1)]
+            locs = torch.tensor([1 + r * CTX + s - 1 for r, s in zip((0, 1), seqs)], device=DEV)
+            b = ForwardBatch(ForwardMode.DECODE, None, None, torch.tensor([0, 1], device=DEV),
+                             torch.tensor(seqs, device=DEV), locs if mode == "quest" else None, rtp, kvp, be)
+            be.init_forward_metadata(b)
+            for layer in range(L):
+                kn = torch.stack([kk[layer, r, s - 1] for r, s in zip((0, 1), seqs)]).to(DEV)
+                vn = torch.stack([vv[layer, r, s - 1] for r, s in zip((0, 1), seqs)]).to(DEV)
+                res.append(be.forward_decode(qq[step, layer].to(DEV), kn, vn, Layer(layer), b).cpu())
+        outs[mode] = torch.stack(res)
+        if mode == "quest_hisparse":
+            st = be.coord.stats
+            assert st.misses > 0 and st.hits > 0
+    assert torch.equal(outs["quest"], outs["quest_hisparse"])
