@@ -23,6 +23,9 @@ FLAGS = [
     "-shared",
     # packed fp32 VALU ops stay off (the compiler would form v_pk_*_f32 on its own)
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # no multiply-add contraction: the page scores round each product and each sum
+    # separately, in a fixed order, to match the oracle bit for bit
+    "-ffp-contract=off",
 ]
 
 

@@ -3,7 +3,7 @@
 // token's K/V, select the positions, gather through req_to_token and attend.
 //
 // Four launches on one stream, each consuming the previous one's output:
-//   score (all CUs) -> select + new-token store (one wave per request)
+//   score (all CUs) -> select + new-token store (one block per request)
 //   -> chunk attention (MFMA) -> merge.
 // The new token's K/V is written by the select launch, which runs before the
 // attention launch reads the pool; the scoring launch never reads the pool.

@@ -64,6 +64,12 @@ __device__ inline uint32_t orderable(float f) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
+// 64-bit selection key: order-preserving score in the high word, ~page in the
+// low word, so "larger key" = higher score, then lower page index.
+__device__ inline uint64_t sel_key(uint32_t score_key, int page) {
+  return ((uint64_t)score_key << 32) | (uint32_t)(~(uint32_t)page);
+}
+
 inline int dtype_size(int dtype) { return dtype == QQ_DTYPE_BF16 ? 2 : 4; }
 inline bool dtype_ok(int dtype) { return dtype == QQ_DTYPE_BF16 || dtype == QQ_DTYPE_F32; }
 

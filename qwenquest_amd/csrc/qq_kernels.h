@@ -55,6 +55,10 @@ struct AttnArgs {
 // Page scoring + selection + layout of one layer (qq_quest_retrieve_topk).
 int launch_retrieve(const SelectArgs& a, int bs, hipStream_t stream);
 
+// Page scoring only (scores of long requests' candidate pages); with
+// `store_new` the new token's K/V is stored as well (blocks x == 0).
+int launch_score(const SelectArgs& a, int bs, bool store_new, hipStream_t stream);
+
 // Chunk attention + merge; `workspace` holds the (m, l, o) partials.
 int launch_attention(AttnArgs& a, int kv_dtype, int bs, int64_t workspace_bytes, void* workspace,
                      hipStream_t stream, const char* what);

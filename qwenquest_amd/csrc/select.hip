@@ -216,15 +216,16 @@ __device__ inline void block_qbar(float* s_q, const SelectArgs& a, int b) {
 // 8 pages.  The bounds loads are issued first; q-bar is then computed once per
 // block into LDS while they are in flight (the barrier does not wait for them).
 template <int M>
-__global__ __launch_bounds__(kThreads) void score_candidates_kernel(SelectArgs a) {
+__global__ __launch_bounds__(kThreads) void score_candidates_kernel(SelectArgs a, int store_new) {
   const int b = blockIdx.y;
+  // the three per-request words are loaded together, before any branch on them
   const int64_t s = a.seq[b];
-  if (s <= a.top_k || a.k_sel == 0) return;  // dense layout / recent window only
   const int lim = min(a.limit[b], a.MP);
-  const int p0 = blockIdx.x * a.ppb;
-  if (p0 >= lim) return;
   const int64_t req = a.rpi[b];
-  if (req < 0 || req >= a.R) return;
+  if (store_new && blockIdx.x == 0) store_new_token(a, b);
+  const int p0 = blockIdx.x * a.ppb;
+  // dense layout / recent window only / no candidates here / no request slot
+  if (s <= a.top_k || a.k_sel == 0 || p0 >= lim || req < 0 || req >= a.R) return;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int pw = p0 + wave * 8;  // this wave's 8 pages
   const uint32_t* pbase = a.bounds_layer + req * a.MP * a.C;
@@ -245,6 +246,67 @@ __global__ __launch_bounds__(kThreads) void score_candidates_kernel(SelectArgs a
   float acc[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = lane_partial<M>(w[i], qreg, lane, a.m, a.C);
+  const float v = reduce8_pages(acc, lane);
+  const int p = pw + (lane >> 3);
+  if ((lane & 7) == 0 && p < lim) a.scores[(int64_t)b * a.MP + p] = v;
+}
+
+// score_candidates_kernel for KV*D == 64*M (M a multiple of 4): lane l holds
+// channels [l*M, l*M + M) as M/4 16-byte loads.  The page addresses are wave
+// uniform (scalar base + the lane's offset), min-or-max is one byte permute per
+// channel picked by q-bar's sign, and the products and sums are the same fp32
+// operations in the same order as lane_partial.  Pages past the candidate limit
+// re-read the limit's last page and are not stored, so every load is issued
+// unconditionally.
+template <int M>
+__global__ __launch_bounds__(kThreads) void score_pages_fast_kernel(SelectArgs a, int store_new) {
+  static_assert(M % 4 == 0, "16-byte lane loads");
+  constexpr int C = 64 * M;
+  const int b = blockIdx.y;
+  const int64_t s = a.seq[b];
+  const int lim = min(a.limit[b], a.MP);
+  const int64_t req = a.rpi[b];
+  if (store_new && blockIdx.x == 0) store_new_token(a, b);
+  const int p0 = blockIdx.x * a.ppb;
+  if (s <= a.top_k || a.k_sel == 0 || p0 >= lim || req < 0 || req >= a.R) return;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int pw = p0 + wave * 8;  // this wave's 8 pages
+  const uint32_t* pbase = a.bounds_layer + req * a.MP * C;
+  const uint32_t lane_bytes = (uint32_t)lane * (M * 4);
+  uint32_t w[8][M];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const char* page = reinterpret_cast<const char*>(pbase + (int64_t)min(pw + i, lim - 1) * C);
+#pragma unroll
+    for (int j = 0; j < M / 4; ++j) {
+      const uint4 v = *reinterpret_cast<const uint4*>(page + lane_bytes + 16 * j);
+      w[i][4 * j] = v.x;
+      w[i][4 * j + 1] = v.y;
+      w[i][4 * j + 2] = v.z;
+      w[i][4 * j + 3] = v.w;
+    }
+  }
+  __shared__ float s_q[kMaxC];
+  block_qbar(s_q, a, b);
+  __syncthreads();
+  if (pw >= lim) return;
+  float qreg[M];
+  uint32_t sel[M];  // v_perm selector: max (high half) for q >= 0, else min, into bits 31:16
+#pragma unroll
+  for (int j = 0; j < M; ++j) {
+    qreg[j] = s_q[lane * M + j];
+    sel[j] = qreg[j] >= 0.0f ? 0x03020C0Cu : 0x01000C0Cu;
+  }
+  float acc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    float t = __fmul_rn(qreg[0], __uint_as_float(__builtin_amdgcn_perm(w[i][0], w[i][0], sel[0])));
+#pragma unroll
+    for (int j = 1; j < M; ++j)
+      t = __fadd_rn(t, __fmul_rn(qreg[j], __uint_as_float(__builtin_amdgcn_perm(w[i][j], w[i][j], sel[j]))));
+    acc[i] = t;
+  }
   const float v = reduce8_pages(acc, lane);
   const int p = pw + (lane >> 3);
   if ((lane & 7) == 0 && p < lim) a.scores[(int64_t)b * a.MP + p] = v;
@@ -358,12 +420,6 @@ __global__ __launch_bounds__(kThreads) void select_layout_kernel(SelectArgs a) {
   write_recent(pos + (int64_t)k * P, s, P);
 }
 
-// 64-bit selection key: order-preserving score in the high word, ~page in the
-// low word, so "larger key" = higher score, then lower page index.
-__device__ inline uint64_t sel_key(uint32_t score_key, int page) {
-  return ((uint64_t)score_key << 32) | (uint32_t)(~(uint32_t)page);
-}
-
 // Top k <= 64 pages of n_eff <= 256*KPT keys, one block per request:
 //   1. each thread holds KPT keys (pages tid + 256 i) and their max;
 //   2. per wave, T_w = the k-th largest of its 64 lane maxima (LDS rank
@@ -378,8 +434,20 @@ template <int KPT>
 __global__ __launch_bounds__(kThreads) void select_filter_kernel(SelectArgs a) {
   const int b = blockIdx.x;
   const int tid = threadIdx.x;
-  store_new_token(a, b);
+  // Every load of the selection is issued up front: the request words and all
+  // of the request's score slots (those past the candidate limit are masked
+  // below), so the block waits for one memory round trip, not three.
   const int64_t s = a.seq[b];
+  const int64_t req = a.rpi[b];
+  const int lim_raw = a.limit[b];
+  const float* sc = a.scores + (int64_t)b * a.MP;
+  float sv[KPT];
+#pragma unroll
+  for (int i = 0; i < KPT; ++i) {
+    const int p = tid + kThreads * i;
+    sv[i] = p < a.MP ? sc[p] : 0.0f;
+  }
+  store_new_token(a, b);
   int32_t* pos = a.positions + (int64_t)b * a.top_k;
   if (s <= a.top_k) {
     for (int j = tid; j < a.top_k; j += kThreads) pos[j] = (int32_t)min((int64_t)j, max(s - 1, (int64_t)0));
@@ -390,19 +458,10 @@ __global__ __launch_bounds__(kThreads) void select_filter_kernel(SelectArgs a) {
     write_recent(pos, s, a.P);
     return;
   }
-  const int64_t req = a.rpi[b];
-  const int lim = (req >= 0 && req < a.R) ? min(a.limit[b], a.MP) : 0;
+  const int lim = (req >= 0 && req < a.R) ? min(lim_raw, a.MP) : 0;
   const int n_eff = max(lim, k);
-  const float* sc = a.scores + (int64_t)b * a.MP;
   constexpr uint32_t kNegInfKey = 0x007FFFFFu;  // orderable(-inf): masked pages (quest.py:451)
   const int wave = tid >> 6, lane = tid & 63;
-
-  float sv[KPT];
-#pragma unroll
-  for (int i = 0; i < KPT; ++i) {
-    const int p = tid + kThreads * i;
-    sv[i] = p < lim ? sc[p] : 0.0f;
-  }
   uint64_t key[KPT];
   uint64_t tmax = 0ull;
 #pragma unroll
@@ -413,7 +472,7 @@ __global__ __launch_bounds__(kThreads) void select_filter_kernel(SelectArgs a) {
   }
   __shared__ uint64_t s_max[kThreads];
   __shared__ uint64_t s_tw[kWaves];
-  __shared__ uint64_t s_cand[kWaves][64 * KPT];
+  __shared__ uint64_t s_cand[kWaves][64 * KPT + 8];
   __shared__ int s_cnt[kWaves];
   __shared__ int s_order[64];
   s_max[tid] = tmax;
@@ -439,6 +498,9 @@ __global__ __launch_bounds__(kThreads) void select_filter_kernel(SelectArgs a) {
     base += __popcll(mask);
   }
   if (lane == 0) s_cnt[wave] = base;
+  // zero keys up to a multiple of 8 (a zero key ranks above nothing), so the
+  // ranking below reads 8 keys per step and waits for LDS once per step
+  if (lane < 8) s_cand[wave][base + lane] = 0ull;
   __syncthreads();
   int cnt[kWaves], total = 0;
 #pragma unroll
@@ -452,8 +514,13 @@ __global__ __launch_bounds__(kThreads) void select_filter_kernel(SelectArgs a) {
     const uint64_t ci = s_cand[w0][off];
     int r = 0;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w)
-      for (int j = 0; j < cnt[w]; ++j) r += s_cand[w][j] > ci;
+    for (int w = 0; w < kWaves; ++w) {
+      const int padded = (cnt[w] + 7) & ~7;
+      for (int j = 0; j < padded; j += 8) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) r += s_cand[w][j + u] > ci;
+      }
+    }
     if (r < k) s_order[r] = (int)(~(uint32_t)ci);
   }
   __syncthreads();
@@ -526,19 +593,32 @@ static void launch_select(const SelectArgs& a, int bs, int max_pages, int k_sel,
     select_layout_kernel<<<bs, kThreads, 0, s>>>(a);
 }
 
-int launch_retrieve(const SelectArgs& a, int bs, hipStream_t s) {
+int launch_score(const SelectArgs& a, int bs, bool store_new, hipStream_t s) {
   dim3 grid(max(1, ceil_div(a.MP, kPagesPerBlock)), bs);
   const int M = (a.C + 63) / 64;
-  if (M <= 1)
-    score_candidates_kernel<1><<<grid, kThreads, 0, s>>>(a);
+  const int st = store_new ? 1 : 0;
+  if (a.C == 512)
+    score_pages_fast_kernel<8><<<grid, kThreads, 0, s>>>(a, st);
+  else if (a.C == 1024)
+    score_pages_fast_kernel<16><<<grid, kThreads, 0, s>>>(a, st);
+  else if (a.C == 256)
+    score_pages_fast_kernel<4><<<grid, kThreads, 0, s>>>(a, st);
+  else if (M <= 1)
+    score_candidates_kernel<1><<<grid, kThreads, 0, s>>>(a, st);
   else if (M <= 2)
-    score_candidates_kernel<2><<<grid, kThreads, 0, s>>>(a);
+    score_candidates_kernel<2><<<grid, kThreads, 0, s>>>(a, st);
   else if (M <= 4)
-    score_candidates_kernel<4><<<grid, kThreads, 0, s>>>(a);
+    score_candidates_kernel<4><<<grid, kThreads, 0, s>>>(a, st);
   else if (M <= 8)
-    score_candidates_kernel<8><<<grid, kThreads, 0, s>>>(a);
+    score_candidates_kernel<8><<<grid, kThreads, 0, s>>>(a, st);
   else
-    score_candidates_kernel<16><<<grid, kThreads, 0, s>>>(a);
+    score_candidates_kernel<16><<<grid, kThreads, 0, s>>>(a, st);
+  return check_launch("quest page scores");
+}
+
+int launch_retrieve(const SelectArgs& a, int bs, hipStream_t s) {
+  const int st = launch_score(a, bs, false, s);
+  if (st != QQ_OK) return st;
   launch_select(a, bs, a.MP, a.k_sel, s);
   return check_launch("quest retrieve");
 }

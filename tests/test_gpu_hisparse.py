@@ -209,16 +209,18 @@ def test_golden_200_step_trace_through_the_kernels():
 
 
 @pytest.mark.parametrize("avoid", [False, True])
-def test_quest_hisparse_is_bit_identical_to_quest(avoid):
+@pytest.mark.parametrize("H,KVH,DIM", [(8, 2, 16), (16, 2, 128)])
+def test_quest_hisparse_is_bit_identical_to_quest(avoid, H, KVH, DIM):
     """reference tests/test_engine.py:59-69 and test_bf16.py:27-43 at the backend boundary:
     the same q/k/v through QuestOnlyBackend and QuestHiSparseBackend over many decode steps
-    (the hot buffer must swap) give bit-identical outputs."""
+    (the hot buffer must swap) give bit-identical outputs.  head_dim 128 runs the
+    merge-free kernel in both modes (selection fused in quest, rows given in hisparse)."""
     from qwenquest_amd.attention.quest_hisparse import QuestHiSparseBackend
     from qwenquest_amd.attention.quest_only import QuestOnlyBackend
     from qwenquest_amd.batch import ForwardBatch, ForwardMode
     from qwenquest_amd.memory import MHATokenToKVPool, ReqToTokenPool
 
-    L, H, KVH, DIM, CTX = 3, 8, 2, 16, 256
+    L, CTX = 3, 256
     cfg = {"algorithm": "quest", "top_k": 32, "quest_page_size": 8, "device_buffer_size": 48,
            "avoid_recent_overlap": avoid}
     gen = torch.Generator().manual_seed(3)

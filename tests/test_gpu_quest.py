@@ -173,6 +173,32 @@ def test_page_scores_bit_exact_in_canonical_order(kv, d, dtype):
     assert np.array_equal(np.isneginf(got), np.isneginf(ref))
 
 
+@pytest.mark.parametrize("kv,d", [(4, 128), (8, 128), (4, 64), (2, 32), (5, 32), (3, 8)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_retrieve_scores_bit_exact_in_canonical_order(kv, d, dtype):
+    """The scores retrieve_topk ranks (its scoring launch, fused with the GQA mean) equal
+    the oracle's bit for bit on every candidate page, for the 16-byte lane-load shapes
+    (KV*D = 256, 512, 1024) and the general ones; 3 requests of different limits."""
+    P, heads = 16, kv * 4
+    q, st = new_quest(64, P, 1, 3, 4096, kv, d)
+    pool = rand_bf16((4096, kv, d), seed=kv * d + 1, mean=rand_bf16((4096, 1, 1), seed=3, scale=0.5))
+    lens = (4000, 1500, 700)
+    for r, n in enumerate(lens):
+        q.update_prefill_representations(0, r, pool.to(DEV), torch.arange(n, device=DEV))
+        st.update_prefill_representations(0, r, bf16_bits(pool), np.arange(n))
+    queries = (rand_bf16((3, heads, d), seed=kv + d) * 2).to(dtype)
+    reqs, seqs = [2, 0, 1], [701, 4001, 1501]
+    q.prepare_step(torch.tensor(seqs, device=DEV))
+    q.retrieve_topk(queries.to(DEV), 0, torch.tensor(reqs, device=DEV), torch.tensor(seqs, device=DEV))
+    got = q._scores_ws[:3].cpu().numpy()
+    qbar = oq.group_queries(queries.float().numpy(), kv, d, is_bf16=dtype == torch.bfloat16)
+    lay = st.prepare_step(seqs)
+    for i, r in enumerate(reqs):
+        lim = int(lay.candidate_limit[i])
+        ref = oq.page_scores(qbar[i : i + 1], st.page_k_bounds[0, [r], :lim])[0]
+        assert np.array_equal((got[i, :lim] + np.float32(0)).view(np.uint32), (ref + np.float32(0)).view(np.uint32))
+
+
 # ------------------------------------------------------------------ selection
 
 
@@ -403,7 +429,21 @@ def test_determinism_bitwise():
     assert torch.equal(a, b)
 
 
-def test_forward_decode_fused_path_engine_flow():
+# (layers, q heads, kv heads, head_dim, page, top_k, ctx, prompts, steps): the first runs
+# the four-launch path (head_dim 16), the others the merge-free kernel (bf16, head_dim
+# 128): the benchmark's shape with long, short, exactly-top_k and one-past requests; a
+# page of 16 with top_k 48 (layout width not a multiple of 32); G = 1; G = 8 with 8 KV heads.
+ENGINE_FLOWS = [
+    (2, 8, 2, 16, 8, 32, 256, {1: 37, 2: 60}, 40),
+    (1, 32, 4, 128, 64, 2048, 9000, {0: 8800, 1: 2046, 2: 2047, 3: 1000}, 4),
+    (1, 16, 4, 128, 16, 48, 600, {0: 500, 1: 40, 2: 47}, 12),
+    (1, 4, 4, 128, 8, 64, 700, {0: 650, 2: 63}, 6),
+    (1, 64, 8, 128, 32, 256, 1500, {0: 1400, 1: 255}, 4),
+]
+
+
+@pytest.mark.parametrize("flow", range(len(ENGINE_FLOWS)))
+def test_forward_decode_fused_path_engine_flow(flow):
     """QuestOnlyBackend.forward_decode (one C call: new K/V store + select + attention) over
     decode steps whose K/V only arrives through forward_decode, vs the oracle; with trace."""
     from qwenquest_amd.attention.quest_only import QuestOnlyBackend
@@ -411,19 +451,19 @@ def test_forward_decode_fused_path_engine_flow():
     from qwenquest_amd.memory import MHATokenToKVPool, ReqToTokenPool
     from qwenquest_amd.quest import QuestTrace
 
-    L, H, KV, D, P, TOP_K, CTX = 2, 8, 2, 16, 8, 32, 256
+    L, H, KV, D, P, TOP_K, CTX, prompt, steps = ENGINE_FLOWS[flow]
+    nreq = max(prompt) + 1
     for avoid in (False, True):
-        rtp = ReqToTokenPool(3, CTX, DEV)
-        kvp = MHATokenToKVPool(3 * CTX, L, KV, D, torch.bfloat16, DEV)
+        rtp = ReqToTokenPool(nreq, CTX, DEV)
+        kvp = MHATokenToKVPool(nreq * CTX, L, KV, D, torch.bfloat16, DEV)
         be = QuestOnlyBackend(rtp, kvp, {"algorithm": "quest", "top_k": TOP_K, "quest_page_size": P,
                                          "avoid_recent_overlap": avoid})
         be.quest.trace = QuestTrace()
         st = oq.QuestState(TOP_K, P, avoid_recent_overlap=avoid)
-        st.init_storage(0, L, 3, CTX, KV, D)
-        kk = rand_bf16((L, 3 * CTX + 1, KV, D), seed=41)
-        vv = rand_bf16((L, 3 * CTX + 1, KV, D), seed=42)
+        st.init_storage(0, L, nreq, CTX, KV, D)
+        kk = rand_bf16((L, nreq * CTX + 1, KV, D), seed=41)
+        vv = rand_bf16((L, nreq * CTX + 1, KV, D), seed=42)
         kb, vb = bf16.to_f32(bf16_bits(kk)), bf16.to_f32(bf16_bits(vv))
-        prompt = {1: 37, 2: 60}
         for r, n in prompt.items():
             rows = torch.arange(1 + r * CTX, 1 + r * CTX + n)
             rtp.req_to_token[r] = torch.arange(1 + r * CTX, 1 + (r + 1) * CTX, dtype=torch.int32)
@@ -433,13 +473,13 @@ def test_forward_decode_fused_path_engine_flow():
             be._skip_first_decode_update[r] = True
             for layer in range(L):
                 st.update_prefill_representations(layer, r, bf16_bits(kk[layer]), rows.numpy())
-        reqs = [1, 2]
+        reqs = sorted(prompt)
 
         class Layer:
             def __init__(self, i):
                 self.layer_id, self.scaling = i, D**-0.5
 
-        for step in range(40):
+        for step in range(steps):
             seqs = [prompt[r] + step + 1 for r in reqs]
             locs = torch.tensor([1 + r * CTX + s - 1 for r, s in zip(reqs, seqs)], device=DEV)
             batch = ForwardBatch(ForwardMode.DECODE, None, None, torch.tensor(reqs, device=DEV),
@@ -450,12 +490,12 @@ def test_forward_decode_fused_path_engine_flow():
                     st.update_decode_representations(layer, reqs, bf16_bits(kk[layer]), (locs - 1).cpu().numpy())
                 st.maybe_finalize_decode_representations(reqs)
             st.prepare_step(seqs)
-            q = rand_bf16((2, H, D), seed=300 + step)
+            q = rand_bf16((len(reqs), H, D), seed=300 + step)
             for layer in range(L):
                 lc = locs.cpu()
                 out = be.forward_decode(q.to(DEV), kk[layer, lc].to(DEV), vv[layer, lc].to(DEV), Layer(layer), batch)
                 ref_pos, ref_actual, _ = st.retrieve_topk(q.float().numpy(), layer, reqs)
-                rec = be.quest.trace.records[-2:]
+                rec = be.quest.trace.records[-len(reqs):]
                 for i, r in enumerate(reqs):
                     n = int(ref_actual[i])
                     assert np.array_equal(rec[i].positions.numpy(), ref_pos[i, :n]), f"step {step} L{layer} r{r}"
@@ -465,5 +505,47 @@ def test_forward_decode_fused_path_engine_flow():
         assert_state_equal(be.quest, st)
         # the new tokens really went to the pool
         torch.cuda.synchronize()
-        last = [1 + r * CTX + prompt[r] + 39 for r in reqs]
+        last = [1 + r * CTX + prompt[r] + steps - 1 for r in reqs]
         assert torch.equal(kvp.k_all[:, last].cpu(), kk[:, last])
+
+
+def test_positions_and_rows_entries_are_bit_identical():
+    """qq_quest_decode_attention (positions through req_to_token) and
+    qq_decode_attention_rows (rows given) on the same rows give the same bits, with
+    ragged lengths (0, 1, 31, 2048), duplicated and out-of-range positions."""
+    from qwenquest_amd.attention.ops import decode_attention_rows
+    from qwenquest_amd.attention.quest_only import QuestOnlyBackend
+    from qwenquest_amd.memory import MHATokenToKVPool, ReqToTokenPool
+
+    H, KV, D, CTX, W = 32, 4, 128, 3000, 2048
+    rtp = ReqToTokenPool(5, CTX, DEV)
+    kvp = MHATokenToKVPool(5 * CTX, 1, KV, D, torch.bfloat16, DEV)
+    be = QuestOnlyBackend(rtp, kvp, {"algorithm": "quest", "top_k": W, "quest_page_size": 64})
+    gen = torch.Generator().manual_seed(5)
+    kvp.k_all.copy_(rand_bf16(tuple(kvp.k_all.shape), seed=51).to(DEV))
+    kvp.v_all.copy_(rand_bf16(tuple(kvp.v_all.shape), seed=52).to(DEV))
+    r2t = torch.randperm(5 * CTX, generator=gen)[: 5 * CTX].view(5, CTX).to(torch.int32) + 1
+    rtp.req_to_token.copy_(r2t.to(DEV))
+    reqs = torch.tensor([4, 0, 2, 3], dtype=torch.int64)
+    actual = torch.tensor([2048, 0, 1, 31], dtype=torch.int32)
+    pos = torch.randint(0, CTX, (4, W), generator=gen, dtype=torch.int32)
+    pos[0, 5] = pos[0, 4]
+    pos[3, 7] = CTX + 5  # outside req_to_token: row 0
+    q = rand_bf16((4, H, D), seed=53)
+
+    class Layer:
+        layer_id, scaling = 0, D**-0.5
+
+    out_pos = be.sparse_attention(q.to(DEV), Layer(), reqs.to(DEV), pos.to(DEV), actual.to(DEV), 4)
+    p64 = pos.to(torch.int64)
+    rows = torch.where(p64 < CTX, r2t[reqs[:, None], p64.clamp(max=CTX - 1)].to(torch.int64), 0)
+    out_rows = decode_attention_rows(q.to(DEV), kvp.k_buffer[0], kvp.v_buffer[0], rows.to(DEV), actual.to(DEV), D**-0.5)
+    assert torch.equal(out_pos, out_rows)
+    kb = bf16.to_f32(bf16_bits(kvp.k_all[0].cpu()))
+    vb = bf16.to_f32(bf16_bits(kvp.v_all[0].cpu()))
+    got = out_rows.float().cpu().numpy()
+    for i in (0, 2, 3):
+        r = rows[i, : int(actual[i])].numpy()
+        ref = oa.decode_attention(q[i].float().numpy(), kb[r], vb[r], D**-0.5)
+        assert np.abs(got[i] - ref).max() < 2e-2
+    assert not got[1].any()  # no rows: zeros
