@@ -164,14 +164,27 @@ int qq_decode_attention_rows(const void* q, int q_dtype, int64_t q_batch_stride,
                              int64_t rows_stride, const int32_t* actual_lens, int bs, float scale,
                              void* out, void* workspace, int64_t workspace_bytes, void* stream);
 
+/* Bytes of the sync buffer qq_quest_forward_decode's two-launch path uses for
+ * `bs` requests (one counter per request and per (request, KV head), each on
+ * its own 128-byte line).  The caller zeroes it once; every call leaves it
+ * zeroed again. */
+int64_t qq_quest_layer_step_sync_bytes(int bs, int kv_heads);
+
 /* Replaces QuestOnlyBackend.forward_decode (src/qwenquest/attention/quest_only.py:132-159)
- * for one layer in four launches: the new tokens' K/V (k_new/v_new [bs, KV, D])
- * go to rows out_cache_loc of k_layer/v_layer (memory.py:114-120; skipped when
- * k_new is NULL), then retrieve_topk (quest.py:409-464) writes positions
- * [bs, top_k], then attention over req_to_token[req, positions[:n]] writes out
- * [bs, H*D] (ops.py:48-66).  seq_lens / candidate_limit / actual_lens are the
- * step's prepare_step outputs; workspace sized by
- * qq_decode_attention_workspace_bytes(bs, top_k, H, D). */
+ * for one layer: the new tokens' K/V (k_new/v_new [bs, KV, D]) go to rows
+ * out_cache_loc of k_layer/v_layer (memory.py:114-120; skipped when k_new is
+ * NULL), retrieve_topk (quest.py:409-464) writes positions [bs, top_k], and
+ * attention over req_to_token[req, positions[:n]] writes out [bs, H*D]
+ * (ops.py:48-66; rows equal to out_cache_loc[i] attend the new K/V, as after
+ * set_kv_buffer).  seq_lens / candidate_limit / actual_lens are the step's
+ * prepare_step outputs; workspace sized by
+ * qq_decode_attention_workspace_bytes(bs, top_k, H, D).
+ * With `sync` (>= qq_quest_layer_step_sync_bytes, zeroed before the first
+ * call), bf16 tensors, KV*D = 4*128, page 64, top_k/P - 1 <= 64 and
+ * max_pages <= 4096, the layer runs as two launches (score + select, then
+ * attention + merge; the selection and the merge hand off inside them);
+ * otherwise, or with sync == NULL, as four launches.  Calls sharing one sync
+ * buffer must not overlap (one stream). */
 int qq_quest_forward_decode(const void* q, int q_dtype, int64_t q_batch_stride, int num_q_heads,
                             const void* k_new, const void* v_new, int new_dtype,
                             const int64_t* out_cache_loc, void* k_layer, void* v_layer,
@@ -182,7 +195,7 @@ int qq_quest_forward_decode(const void* q, int q_dtype, int64_t q_batch_stride, 
                             int page_size, int top_k, const int32_t* req_to_token,
                             int64_t req_to_token_stride, int64_t req_to_token_rows, float scale,
                             float* scores_ws, int32_t* positions, void* out, void* workspace,
-                            int64_t workspace_bytes, void* stream);
+                            int64_t workspace_bytes, void* sync, int64_t sync_bytes, void* stream);
 
 /* Replaces MHATokenToKVPool.set_kv_buffer (src/qwenquest/memory.py:114-120):
  * k_layer[locs[i]] = k[i], v_layer[locs[i]] = v[i] (row = KV*D elements),

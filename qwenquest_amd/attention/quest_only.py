@@ -64,6 +64,10 @@ class QuestOnlyBackend(AttentionBackend):
         self._skip_first_decode_update = torch.zeros(req_to_token_pool.size, dtype=torch.bool, device=device)
         self._positions = torch.empty((req_to_token_pool.size, cfg.top_k), dtype=torch.int32, device=device)
         self._attn_ws = AttentionWorkspace(device)
+        # counters of the fused (two-launch) layer step: zeroed once, left zeroed by every
+        # call (set to None to run the layer as four launches)
+        sync_bytes = int(_lib.load().qq_quest_layer_step_sync_bytes(req_to_token_pool.size, token_to_kv_pool.kv_heads))
+        self._step_sync = torch.zeros(max(sync_bytes, 4), dtype=torch.uint8, device=device)
 
     # ---------------------------------------------------------------- per step
 
@@ -133,6 +137,7 @@ class QuestOnlyBackend(AttentionBackend):
         buf = self._attn_ws.get(bs, quest.top_k, heads, dim)
         out = torch.empty((bs, heads * dim), dtype=q3.dtype, device=q3.device)
         r2t = self.req_to_token
+        sync = self._step_sync  # None: the four-launch path
         _lib.call(
             "qq_quest_forward_decode", _lib.ptr(q3), _lib.dtype_code(q3.dtype), q3.stride(0), heads,
             _lib.ptr(kn), _lib.ptr(vn), _lib.dtype_code(kn.dtype), _lib.ptr(loc), _lib.ptr(k_buf),
@@ -141,7 +146,8 @@ class QuestOnlyBackend(AttentionBackend):
             _lib.ptr(step.candidate_limit_i32), _lib.ptr(step.actual_lens), bs, quest.max_reqs,
             quest.max_pages_per_req, quest.kv_heads, quest.head_dim, quest.page_size, quest.top_k,
             _lib.ptr(r2t), r2t.stride(0), r2t.shape[0], float(layer.scaling), _lib.ptr(quest._scores_ws),
-            _lib.ptr(self._positions), _lib.ptr(out), _lib.ptr(buf), buf.numel(), _lib.stream(q3.device),
+            _lib.ptr(self._positions), _lib.ptr(out), _lib.ptr(buf), buf.numel(), _lib.ptr(sync),
+            0 if sync is None else sync.numel(), _lib.stream(q3.device),
         )
         if quest.trace is not None:
             quest._record(layer.layer_id, rpi, step, self._positions[:bs])

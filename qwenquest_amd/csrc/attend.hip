@@ -19,12 +19,12 @@
 //        transposed 4x8 in registers, channel d = 8*(lane % 16) + e.
 //      Other shapes / fp32 use a scalar kernel with the same partial format.
 //   2. merge kernel, grid (H, bs): out = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c.
-#include "qq_kernels.h"
+#include "qq_quest_dev.h"
 
 namespace qq {
 namespace {
 
-constexpr int kThreads = 256;
+constexpr int kThreads = kBlock;
 constexpr int kChunk = 64;
 
 
@@ -105,14 +105,6 @@ __global__ __launch_bounds__(kThreads) void attn_chunk_kernel(AttnArgs a) {
 
 }
 
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef short short4_t __attribute__((ext_vector_type(4)));
-typedef float float4_t __attribute__((ext_vector_type(4)));
-
-constexpr float kLog2e = 1.4426950408889634f;
-constexpr float kLn2 = 0.6931471805599453f;
-constexpr int kMfmaDim = 128;
-
 __device__ inline int64_t chunk_row(const AttnArgs& a, int b, int i) {
   int64_t row;
   if (a.rows) {
@@ -138,99 +130,22 @@ __global__ __launch_bounds__(64 * KV) void attn_mfma_kernel(AttnArgs a) {
   const int lo = l & 15, hi = l >> 4;
   const int G = a.H / KV;
   constexpr int kRow = KV * kMfmaDim;  // elements per pool row
-  __shared__ int64_t s_rows[kChunk];
-  if (threadIdx.x < kChunk) s_rows[threadIdx.x] = threadIdx.x < cnt ? chunk_row(a, b, r0 + threadIdx.x) : 0;
+  // row pointers per KV head (row base + head * 128 channels)
+  __shared__ const uint16_t* s_kp[KV][kChunk];
+  __shared__ const uint16_t* s_vp[KV][kChunk];
+  if (threadIdx.x < kChunk) {
+    const int64_t row = threadIdx.x < cnt ? chunk_row(a, b, r0 + threadIdx.x) : 0;
+#pragma unroll
+    for (int h = 0; h < KV; ++h) {
+      s_kp[h][threadIdx.x] = static_cast<const uint16_t*>(a.k) + row * kRow + h * kMfmaDim;
+      s_vp[h][threadIdx.x] = static_cast<const uint16_t*>(a.v) + row * kRow + h * kMfmaDim;
+    }
+  }
   __syncthreads();
-
-  // K as the A operand: tile t (16 tokens) x k-step ks (32 channels): 16 bytes per lane.
-  const uint16_t* kbase = static_cast<const uint16_t*>(a.k) + w * kMfmaDim + hi * 8;
-  bf16x8_t ka[4][4];
-#pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    const uint16_t* kp = kbase + s_rows[t * 16 + lo] * kRow;
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) ka[t][ks] = *reinterpret_cast<const bf16x8_t*>(kp + ks * 32);
-  }
-  // V row slices for P V: k-step s (16 tokens), token j of the lane's 4; 16 bytes =
-  // channels 8*lo .. 8*lo + 7 of this KV head (16 lanes cover the 256-byte slice).
-  const uint16_t* vbase = static_cast<const uint16_t*>(a.v) + w * kMfmaDim + lo * 8;
-  uint4 vr[4][4];
-#pragma unroll
-  for (int s = 0; s < 4; ++s)
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      vr[s][j] = *reinterpret_cast<const uint4*>(vbase + s_rows[s * 16 + hi * 4 + j] * kRow);
-  // Q^T as the B operand: query head w*G + lo (zero past G), channels 8*hi + 32*ks.
-  bf16x8_t qb[4];
-  {
-    const uint16_t* qp = static_cast<const uint16_t*>(a.q) + (int64_t)b * a.q_bstride +
-                         (int64_t)(w * G + lo) * kMfmaDim + hi * 8;
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      if (lo < G) {
-        qb[ks] = *reinterpret_cast<const bf16x8_t*>(qp + ks * 32);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) qb[ks][e] = (__bf16)0.0f;
-      }
-    }
-  }
-
-  // S^T[token t*16 + 4*hi + i][head lo] in acc[t][i]
-  float4_t acc[4];
-#pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    acc[t] = float4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
-      acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[t][ks], qb[ks], acc[t], 0, 0, 0);
-  }
-  const float sl2 = a.scale * kLog2e;
-  float mx = -INFINITY;
-#pragma unroll
-  for (int t = 0; t < 4; ++t)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int tok = t * 16 + hi * 4 + i;
-      const float x = tok < cnt ? acc[t][i] * sl2 : -INFINITY;
-      acc[t][i] = x;
-      mx = fmaxf(mx, x);
-    }
-  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-  float sum = 0.0f;
-  short4_t pa[4];
-#pragma unroll
-  for (int t = 0; t < 4; ++t)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint16_t pb = f2bf(exp2f(acc[t][i] - mx));
-      sum += bf2f(pb);
-      pa[t][i] = (short)pb;
-    }
-  sum += __shfl_xor(sum, 16, 64);
-  sum += __shfl_xor(sum, 32, 64);
-
-  // O[head 4*hi + i][d = 8*lo + e] in o[e][i]
+  float mx, sum;
   float4_t o[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) o[e] = float4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    short4_t vb[8];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint4 u = vr[s][j];
-      const uint32_t wv[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-      for (int x = 0; x < 4; ++x) {
-        vb[2 * x][j] = (short)(wv[x] & 0xFFFFu);
-        vb[2 * x + 1][j] = (short)(wv[x] >> 16);
-      }
-    }
-#pragma unroll
-    for (int e = 0; e < 8; ++e) o[e] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa[s], vb[e], o[e], 0, 0, 0);
-  }
+  const uint16_t* qh = static_cast<const uint16_t*>(a.q) + (int64_t)b * a.q_bstride + (int64_t)w * G * kMfmaDim;
+  attn_wave64(s_kp[w], s_vp[w], qh, G, cnt, a.scale * kLog2e, mx, sum, o);
 
   const int64_t part = (int64_t)b * a.max_chunks + c;
 #pragma unroll

@@ -55,6 +55,9 @@ struct AttnArgs {
 // Page scoring + selection + layout of one layer (qq_quest_retrieve_topk).
 int launch_retrieve(const SelectArgs& a, int bs, hipStream_t stream);
 
+// Selection + layout only (one block per request), from scores already in a.scores.
+void launch_select(const SelectArgs& a, int bs, int max_pages, int k_sel, hipStream_t stream);
+
 // Page scoring only (scores of long requests' candidate pages); with
 // `store_new` the new token's K/V is stored as well (blocks x == 0).
 int launch_score(const SelectArgs& a, int bs, bool store_new, hipStream_t stream);

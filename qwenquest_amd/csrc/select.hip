@@ -17,53 +17,16 @@
 // per-thread maxima filters the keys, survivors are rank-counted; otherwise a 4-pass radix
 // select on order-preserving 32-bit keys with ties at the threshold to the
 // lowest page index.
-#include "qq_kernels.h"
+#include "qq_quest_dev.h"
 
 namespace qq {
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kWaves = kThreads / 64;
-constexpr int kMaxC = 1024;    // KV * D
+constexpr int kThreads = kBlock;
 constexpr int kMaxSel = 1024;  // top_k / P - 1
 constexpr int kPagesPerBlock = 32;
 
 
-
-// k_pool[new_locs[b]] = new_k[b] (and V), one row of C elements, converted to the pool dtype.
-__device__ inline void store_new_token(const SelectArgs& a, int b) {
-  if (!a.new_k) return;
-  const int64_t loc = a.new_locs[b];
-  if (loc < 0 || loc >= a.pool_rows) return;
-  const int C = a.C;
-  if (a.new_dtype == QQ_DTYPE_BF16 && a.pool_dtype == QQ_DTYPE_BF16 && C % 8 == 0) {
-    const uint4* ks = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.new_k) + (int64_t)b * C);
-    const uint4* vs = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.new_v) + (int64_t)b * C);
-    uint4* kd = reinterpret_cast<uint4*>(static_cast<uint16_t*>(a.k_pool) + loc * C);
-    uint4* vd = reinterpret_cast<uint4*>(static_cast<uint16_t*>(a.v_pool) + loc * C);
-    for (int e = threadIdx.x; e < C / 8; e += blockDim.x) {
-      kd[e] = ks[e];
-      vd[e] = vs[e];
-    }
-    return;
-  }
-  for (int e = threadIdx.x; e < C; e += blockDim.x) {
-    const float kv = load_as_float(a.new_k, (int64_t)b * C + e, a.new_dtype);
-    const float vv = load_as_float(a.new_v, (int64_t)b * C + e, a.new_dtype);
-    if (a.pool_dtype == QQ_DTYPE_BF16) {
-      static_cast<uint16_t*>(a.k_pool)[loc * C + e] = f2bf(kv);
-      static_cast<uint16_t*>(a.v_pool)[loc * C + e] = f2bf(vv);
-    } else {
-      static_cast<float*>(a.k_pool)[loc * C + e] = kv;
-      static_cast<float*>(a.v_pool)[loc * C + e] = vv;
-    }
-  }
-}
-
-__device__ inline void write_recent(int32_t* pos, int64_t s, int P) {
-  const int64_t start = max(s - P, (int64_t)0);
-  for (int j = threadIdx.x; j < P; j += kThreads) pos[j] = (int32_t)min(start + j, s - 1);
-}
 
 // Block-wide inclusive suffix sum over 256 entries of `v` (in place).
 __device__ inline void suffix_sum_256(uint32_t* v) {
@@ -90,52 +53,6 @@ __device__ inline void prefix_sum_256_exclusive(int* v) {
   __syncthreads();
   v[t] -= mine;
   __syncthreads();
-}
-
-// GQA mean of channel c = h*D + d (quest.py:385-391): fp32 sum over the G query
-// heads of KV head h in head order, divided by G, rounded once to the query
-// dtype.  G == 1 returns the query unchanged.
-__device__ inline float gqa_mean(const void* q, int dtype, int64_t qb, int G, int D, int c) {
-  if (G == 1) return load_as_float(q, qb + c, dtype);
-  const int h = c / D, d = c - h * D;
-  float acc = 0.0f;
-  for (int g = 0; g < G; ++g)
-    acc = __fadd_rn(acc, load_as_float(q, qb + (int64_t)(h * G + g) * D + d, dtype));
-  acc = acc / (float)G;
-  return dtype == QQ_DTYPE_BF16 ? bf2f(f2bf(acc)) : acc;
-}
-
-// Lane partials of 8 pages at once.  acc[p] is this lane's partial of page p
-// (its m channels, summed in order).  The 8 halving trees are interleaved: at
-// level w = 32, 16, 8 each lane keeps half of its pages and adds the partner's
-// (lane l ^ w) partial of them - the pairs are exactly the tree's (i, i + w) -
-// then levels 4, 2, 1 run on one value.  Lane l ends with page l >> 3.
-__device__ inline float reduce8_pages(float (&acc)[8], int lane) {
-  const bool up32 = lane & 32, up16 = lane & 16, up8 = lane & 8;
-  float v4[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const float send = up32 ? acc[j] : acc[4 + j];
-    const float keep = up32 ? acc[4 + j] : acc[j];
-    v4[j] = __fadd_rn(keep, __shfl_xor(send, 32, 64));
-  }
-  float v2[2];
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const float send = up16 ? v4[j] : v4[2 + j];
-    const float keep = up16 ? v4[2 + j] : v4[j];
-    v2[j] = __fadd_rn(keep, __shfl_xor(send, 16, 64));
-  }
-  float v;
-  {
-    const float send = up8 ? v2[0] : v2[1];
-    const float keep = up8 ? v2[1] : v2[0];
-    v = __fadd_rn(keep, __shfl_xor(send, 8, 64));
-  }
-  v = __fadd_rn(v, __shfl_xor(v, 4, 64));
-  v = __fadd_rn(v, __shfl_xor(v, 2, 64));
-  v = __fadd_rn(v, __shfl_xor(v, 1, 64));
-  return v;
 }
 
 // This lane's m channels of one page, products summed in channel order.
@@ -180,36 +97,6 @@ __device__ inline void load_lane_words(uint32_t (&w)[M], const uint32_t* pb, int
       w[j] = (j < m && c < C) ? pb[c] : 0u;
     }
   }
-}
-
-// q-bar of channels [0, C) into LDS, computed once per block (each thread a
-// channel pair when the query is bf16 and D is even: G 4-byte loads).
-__device__ inline void block_qbar(float* s_q, const SelectArgs& a, int b) {
-  const int G = a.H / a.KV;
-  const int64_t qb = (int64_t)b * a.q_bstride;
-  constexpr int kMaxG = 16;
-  if (a.q_dtype == QQ_DTYPE_BF16 && a.D % 2 == 0 && G > 1 && G <= kMaxG) {
-    for (int c = threadIdx.x * 2; c < a.C; c += kThreads * 2) {
-      const int h = c / a.D, d = c - h * a.D;
-      const uint32_t* qp =
-          reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(a.q) + qb + (int64_t)h * G * a.D + d);
-      uint32_t u[kMaxG];
-#pragma unroll
-      for (int g = 0; g < kMaxG; ++g) u[g] = g < G ? qp[(int64_t)g * (a.D / 2)] : 0u;  // all in flight
-      float a0 = 0.0f, a1 = 0.0f;
-#pragma unroll
-      for (int g = 0; g < kMaxG; ++g) {
-        if (g < G) {
-          a0 = __fadd_rn(a0, bf2f((uint16_t)(u[g] & 0xFFFFu)));
-          a1 = __fadd_rn(a1, bf2f((uint16_t)(u[g] >> 16)));
-        }
-      }
-      s_q[c] = bf2f(f2bf(a0 / (float)G));
-      s_q[c + 1] = bf2f(f2bf(a1 / (float)G));
-    }
-    return;
-  }
-  for (int c = threadIdx.x; c < a.C; c += kThreads) s_q[c] = gqa_mean(a.q, a.q_dtype, qb, G, a.D, c);
 }
 
 // Scores the candidate pages [0, candidate_limit) of long requests: each wave
@@ -260,7 +147,6 @@ __global__ __launch_bounds__(kThreads) void score_candidates_kernel(SelectArgs a
 // unconditionally.
 template <int M>
 __global__ __launch_bounds__(kThreads) void score_pages_fast_kernel(SelectArgs a, int store_new) {
-  static_assert(M % 4 == 0, "16-byte lane loads");
   constexpr int C = 64 * M;
   const int b = blockIdx.y;
   const int64_t s = a.seq[b];
@@ -272,42 +158,13 @@ __global__ __launch_bounds__(kThreads) void score_pages_fast_kernel(SelectArgs a
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int pw = p0 + wave * 8;  // this wave's 8 pages
-  const uint32_t* pbase = a.bounds_layer + req * a.MP * C;
-  const uint32_t lane_bytes = (uint32_t)lane * (M * 4);
   uint32_t w[8][M];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const char* page = reinterpret_cast<const char*>(pbase + (int64_t)min(pw + i, lim - 1) * C);
-#pragma unroll
-    for (int j = 0; j < M / 4; ++j) {
-      const uint4 v = *reinterpret_cast<const uint4*>(page + lane_bytes + 16 * j);
-      w[i][4 * j] = v.x;
-      w[i][4 * j + 1] = v.y;
-      w[i][4 * j + 2] = v.z;
-      w[i][4 * j + 3] = v.w;
-    }
-  }
+  load_8pages<M>(w, a.bounds_layer + req * a.MP * C, pw, lim, lane);
   __shared__ float s_q[kMaxC];
   block_qbar(s_q, a, b);
   __syncthreads();
   if (pw >= lim) return;
-  float qreg[M];
-  uint32_t sel[M];  // v_perm selector: max (high half) for q >= 0, else min, into bits 31:16
-#pragma unroll
-  for (int j = 0; j < M; ++j) {
-    qreg[j] = s_q[lane * M + j];
-    sel[j] = qreg[j] >= 0.0f ? 0x03020C0Cu : 0x01000C0Cu;
-  }
-  float acc[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    float t = __fmul_rn(qreg[0], __uint_as_float(__builtin_amdgcn_perm(w[i][0], w[i][0], sel[0])));
-#pragma unroll
-    for (int j = 1; j < M; ++j)
-      t = __fadd_rn(t, __fmul_rn(qreg[j], __uint_as_float(__builtin_amdgcn_perm(w[i][j], w[i][j], sel[j]))));
-    acc[i] = t;
-  }
-  const float v = reduce8_pages(acc, lane);
+  const float v = score_8pages<M>(w, s_q, lane);
   const int p = pw + (lane >> 3);
   if ((lane & 7) == 0 && p < lim) a.scores[(int64_t)b * a.MP + p] = v;
 }
@@ -320,7 +177,7 @@ __global__ __launch_bounds__(kThreads) void select_layout_kernel(SelectArgs a) {
   const int64_t s = a.seq[b];
   int32_t* pos = a.positions + (int64_t)b * a.top_k;
   if (s <= a.top_k) {  // dense layout, quest.py:339-342 / 460
-    for (int j = tid; j < a.top_k; j += kThreads) pos[j] = (int32_t)min((int64_t)j, max(s - 1, (int64_t)0));
+    write_dense(pos, s, a.top_k);
     return;
   }
   const int k = a.k_sel;
@@ -341,7 +198,6 @@ __global__ __launch_bounds__(kThreads) void select_layout_kernel(SelectArgs a) {
   __shared__ int s_order[kMaxSel];
   __shared__ int s_eq[256];
   __shared__ int s_gt;
-  const uint32_t kNegInfKey = 0x007FFFFFu;  // orderable(-inf): masked pages (quest.py:451)
   auto key_of = [&](int p) -> uint32_t {
     return p < lim ? orderable(sc[p]) : kNegInfKey;
   };
@@ -420,16 +276,8 @@ __global__ __launch_bounds__(kThreads) void select_layout_kernel(SelectArgs a) {
   write_recent(pos + (int64_t)k * P, s, P);
 }
 
-// Top k <= 64 pages of n_eff <= 256*KPT keys, one block per request:
-//   1. each thread holds KPT keys (pages tid + 256 i) and their max;
-//   2. per wave, T_w = the k-th largest of its 64 lane maxima (LDS rank
-//      counting; 0 if fewer than k lanes hold keys).  The k largest lane maxima
-//      are k distinct keys >= T_w, so the true k-th largest key is >= T_w, and
-//      every top-k key survives the filter key >= T0 = max_w T_w;
-//   3. each wave compacts its survivors into its own LDS region (ballot +
-//      mbcnt, running base kept in a scalar register: no atomics);
-//   4. each survivor's rank = number of survivors above it; ranks < k give the
-//      pages in (score desc, page asc) order.
+// Top k <= 64 pages of n_eff <= 256*KPT keys, one block per request
+// (select_topk_block), then the layout.
 template <int KPT>
 __global__ __launch_bounds__(kThreads) void select_filter_kernel(SelectArgs a) {
   const int b = blockIdx.x;
@@ -447,89 +295,26 @@ __global__ __launch_bounds__(kThreads) void select_filter_kernel(SelectArgs a) {
     const int p = tid + kThreads * i;
     sv[i] = p < a.MP ? sc[p] : 0.0f;
   }
-  store_new_token(a, b);
   int32_t* pos = a.positions + (int64_t)b * a.top_k;
-  if (s <= a.top_k) {
-    for (int j = tid; j < a.top_k; j += kThreads) pos[j] = (int32_t)min((int64_t)j, max(s - 1, (int64_t)0));
-    return;
-  }
   const int k = a.k_sel;
-  if (k == 0) {
-    write_recent(pos, s, a.P);
+  if (s <= a.top_k || k == 0) {
+    store_new_token(a, b);
+    if (s <= a.top_k)
+      write_dense(pos, s, a.top_k);
+    else
+      write_recent(pos, s, a.P);
     return;
   }
   const int lim = (req >= 0 && req < a.R) ? min(lim_raw, a.MP) : 0;
-  const int n_eff = max(lim, k);
-  constexpr uint32_t kNegInfKey = 0x007FFFFFu;  // orderable(-inf): masked pages (quest.py:451)
-  const int wave = tid >> 6, lane = tid & 63;
-  uint64_t key[KPT];
-  uint64_t tmax = 0ull;
-#pragma unroll
-  for (int i = 0; i < KPT; ++i) {
-    const int p = tid + kThreads * i;
-    key[i] = p < n_eff ? sel_key(p < lim ? orderable(sv[i]) : kNegInfKey, p) : 0ull;
-    tmax = key[i] > tmax ? key[i] : tmax;
-  }
-  __shared__ uint64_t s_max[kThreads];
-  __shared__ uint64_t s_tw[kWaves];
-  __shared__ uint64_t s_cand[kWaves][64 * KPT + 8];
-  __shared__ int s_cnt[kWaves];
-  __shared__ int s_order[64];
-  s_max[tid] = tmax;
-  const int nz = __popcll(__ballot(tmax != 0ull));
-  if (lane == 0) s_tw[wave] = 0ull;
-  __syncthreads();
-  int rank = 0;
-#pragma unroll 16
-  for (int j = 0; j < 64; ++j) rank += s_max[wave * 64 + j] > tmax;
-  if (nz >= k && tmax != 0ull && rank == k - 1) s_tw[wave] = tmax;  // unique: nonzero keys differ
-  __syncthreads();
-  uint64_t t0 = s_tw[0];
-#pragma unroll
-  for (int w = 1; w < kWaves; ++w) t0 = s_tw[w] > t0 ? s_tw[w] : t0;
-  int base = 0;
-#pragma unroll
-  for (int i = 0; i < KPT; ++i) {
-    const bool take = key[i] != 0ull && key[i] >= t0;
-    const uint64_t mask = __ballot(take);
-    if (take)
-      s_cand[wave][base + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
-                                                         __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u))] = key[i];
-    base += __popcll(mask);
-  }
-  if (lane == 0) s_cnt[wave] = base;
-  // zero keys up to a multiple of 8 (a zero key ranks above nothing), so the
-  // ranking below reads 8 keys per step and waits for LDS once per step
-  if (lane < 8) s_cand[wave][base + lane] = 0ull;
-  __syncthreads();
-  int cnt[kWaves], total = 0;
-#pragma unroll
-  for (int w = 0; w < kWaves; ++w) {
-    cnt[w] = s_cnt[w];
-    total += cnt[w];
-  }
-  for (int i = tid; i < total; i += kThreads) {
-    int w0 = 0, off = i;
-    while (off >= cnt[w0]) off -= cnt[w0++];
-    const uint64_t ci = s_cand[w0][off];
-    int r = 0;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
-      const int padded = (cnt[w] + 7) & ~7;
-      for (int j = 0; j < padded; j += 8) {
-#pragma unroll
-        for (int u = 0; u < 8; ++u) r += s_cand[w][j + u] > ci;
-      }
-    }
-    if (r < k) s_order[r] = (int)(~(uint32_t)ci);
-  }
-  __syncthreads();
+  __shared__ SelectSmem<KPT> sm;
+  select_topk_block<KPT>(sv, lim, max(lim, k), k, sm);
   const int P = a.P;
   for (int slot = tid; slot < k * P; slot += kThreads) {
     const int r = slot / P;
-    pos[slot] = s_order[r] * P + (slot - r * P);
+    pos[slot] = sm.order[r] * P + (slot - r * P);
   }
   write_recent(pos + (int64_t)k * P, s, P);
+  store_new_token(a, b);  // the attention launch that reads the pool comes after this one
 }
 
 // group_queries (quest.py:366-391) as its own kernel: out [bs, C] in q's dtype.
@@ -579,7 +364,7 @@ __global__ __launch_bounds__(kThreads) void page_scores_kernel(const void* qbar,
 
 }  // namespace
 
-static void launch_select(const SelectArgs& a, int bs, int max_pages, int k_sel, hipStream_t s) {
+void launch_select(const SelectArgs& a, int bs, int max_pages, int k_sel, hipStream_t s) {
   const int n_max = max(max_pages, k_sel);
   if (k_sel <= 64 && n_max <= 4 * kThreads)
     select_filter_kernel<4><<<bs, kThreads, 0, s>>>(a);

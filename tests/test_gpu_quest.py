@@ -429,13 +429,25 @@ def test_determinism_bitwise():
     assert torch.equal(a, b)
 
 
-# (layers, q heads, kv heads, head_dim, page, top_k, ctx, prompts, steps): the first runs
-# the four-launch path (head_dim 16), the others the merge-free kernel (bf16, head_dim
-# 128): the benchmark's shape with long, short, exactly-top_k and one-past requests; a
-# page of 16 with top_k 48 (layout width not a multiple of 32); G = 1; G = 8 with 8 KV heads.
+def step_counters(be, bs):
+    """The fused layer step's sync buffer: counters only, zero between calls."""
+    return be._step_sync
+
+
+# (layers, q heads, kv heads, head_dim, page, top_k, ctx, prompts, steps).  Flows with
+# bf16, 4 KV heads x 128, page 64 and at most 64 selected pages run the two-launch fused
+# layer step; the others the four-launch path.  Fused: the benchmark's shape with long,
+# short, exactly-top_k and one-past requests; top_k 256 (one attention tile per head);
+# top_k 64 (recent window only); top_k 4160 (64 selected pages, 17 tiles, G = 16); G = 1
+# with a request reaching a multiple of 64 (its newest page becomes a candidate).
+# Four-launch: head_dim 16; page 16 with top_k 48; G = 1 with page 8; 8 KV heads.
 ENGINE_FLOWS = [
     (2, 8, 2, 16, 8, 32, 256, {1: 37, 2: 60}, 40),
     (1, 32, 4, 128, 64, 2048, 9000, {0: 8800, 1: 2046, 2: 2047, 3: 1000}, 4),
+    (1, 32, 4, 128, 64, 256, 3000, {0: 2900, 1: 255, 2: 700}, 6),
+    (1, 4, 4, 128, 64, 64, 700, {0: 650, 1: 63}, 4),
+    (2, 64, 4, 128, 64, 4160, 9000, {0: 8900, 1: 4000, 2: 4159}, 3),
+    (1, 4, 4, 128, 64, 2048, 6000, {0: 4094, 1: 5000}, 4),
     (1, 16, 4, 128, 16, 48, 600, {0: 500, 1: 40, 2: 47}, 12),
     (1, 4, 4, 128, 8, 64, 700, {0: 650, 2: 63}, 6),
     (1, 64, 8, 128, 32, 256, 1500, {0: 1400, 1: 255}, 4),
@@ -507,6 +519,7 @@ def test_forward_decode_fused_path_engine_flow(flow):
         torch.cuda.synchronize()
         last = [1 + r * CTX + prompt[r] + steps - 1 for r in reqs]
         assert torch.equal(kvp.k_all[:, last].cpu(), kk[:, last])
+        assert not step_counters(be, len(reqs)).any()  # the fused path leaves its counters at zero
 
 
 def test_positions_and_rows_entries_are_bit_identical():
@@ -549,3 +562,79 @@ def test_positions_and_rows_entries_are_bit_identical():
         ref = oa.decode_attention(q[i].float().numpy(), kb[r], vb[r], D**-0.5)
         assert np.abs(got[i] - ref).max() < 2e-2
     assert not got[1].any()  # no rows: zeros
+
+
+def test_fused_layer_step_graph_replay_eager_and_four_launch_agree():
+    """The fused (two-launch) layer step replayed from a HIP graph equals its eager run bit for bit
+    (positions and outputs, every replay), the four-launch path gives the same positions
+    and outputs within 2e-2, and the sync counters are back at zero after each step."""
+    from qwenquest_amd.attention.quest_only import QuestOnlyBackend
+    from qwenquest_amd.batch import ForwardBatch, ForwardMode
+    from qwenquest_amd.memory import MHATokenToKVPool, ReqToTokenPool
+
+    L, H, KV, D, P, TOP_K, CTX = 2, 32, 4, 128, 64, 2048, 6200
+    prompts = [6000, 4095, 2047, 1000]
+    B = len(prompts)
+    kk = rand_bf16((L, B * CTX + 1, KV, D), seed=71)
+    vv = rand_bf16((L, B * CTX + 1, KV, D), seed=72)
+    qs = rand_bf16((L, B, H, D), seed=73)
+    kn = rand_bf16((L, B, KV, D), seed=74)
+    vn = rand_bf16((L, B, KV, D), seed=75)
+
+    class Layer:
+        def __init__(self, i):
+            self.layer_id, self.scaling = i, D**-0.5
+
+    def setup(four_launch):
+        rtp = ReqToTokenPool(B, CTX, DEV)
+        kvp = MHATokenToKVPool(B * CTX, L, KV, D, torch.bfloat16, DEV)
+        kvp.k_all.copy_(kk.to(DEV))
+        kvp.v_all.copy_(vv.to(DEV))
+        base = 1 + torch.arange(B, device=DEV, dtype=torch.int64) * CTX
+        rtp.req_to_token.copy_((base[:, None] + torch.arange(CTX, device=DEV)[None]).to(torch.int32))
+        be = QuestOnlyBackend(rtp, kvp, {"algorithm": "quest", "top_k": TOP_K, "quest_page_size": P})
+        if four_launch:
+            be._step_sync = None
+        for r, n in enumerate(prompts):
+            be.quest.update_prefill_representations_fused(r, kvp.k_all, rtp.req_to_token[r, :n])
+            be._skip_first_decode_update[r] = True
+        seq = torch.tensor([n + 1 for n in prompts], device=DEV)
+        loc = torch.empty(B, device=DEV, dtype=torch.int64)
+        batch = ForwardBatch(ForwardMode.DECODE, None, None, torch.arange(B, device=DEV), seq, loc, rtp, kvp, be)
+        outs = torch.empty((L, B, H * D), dtype=torch.bfloat16, device=DEV)
+        pos = torch.empty((L, B, TOP_K), dtype=torch.int32, device=DEV)
+        qd, knd, vnd = qs.to(DEV), kn.to(DEV), vn.to(DEV)
+
+        def step():
+            torch.add(base, seq - 1, out=loc)
+            be.init_forward_metadata(batch)
+            for layer in range(L):
+                outs[layer].copy_(be.forward_decode(qd[layer], knd[layer], vnd[layer], Layer(layer), batch))
+                pos[layer].copy_(be._positions[:B])
+            seq.add_(1)
+
+        return be, step, outs, pos
+
+    runs = {}
+    for name in ("eager", "graph", "four"):
+        be, step, outs, pos = setup(name == "four")
+        step()  # first decode step after prefill, eager
+        run = step
+        if name == "graph":
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                step()
+            run = g.replay
+        res = []
+        for _ in range(70):  # crosses page boundaries: bounds finalized inside the steps
+            run()
+            torch.cuda.synchronize()
+            if be._step_sync is not None:
+                assert not step_counters(be, B).any()
+            res.append((outs.clone(), pos.clone()))
+        runs[name] = res
+    for i, ((oe, pe), (og, pg), (of, pf)) in enumerate(zip(runs["eager"], runs["graph"], runs["four"])):
+        assert torch.equal(pe, pg) and torch.equal(oe, og), f"graph replay {i} differs from eager"
+        assert torch.equal(pe, pf), f"step {i}: four-launch positions differ"
+        assert (oe.float() - of.float()).abs().max().item() < 2e-2, f"step {i}"
