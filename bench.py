@@ -175,23 +175,23 @@ def main() -> int:
     byts = algorithmic_bytes(seqs_timed, P, TOP_K, 2 * KV * D * 2, KV * D * 2 * 2)
     step_frac = byts["headline"] / (us_per_layer_step * 1e-6) / (HBM_PEAK_GBS * 1e9)
 
-    # per-kernel durations: graph of 48 launches of one family at the same shapes
-    quest = be.quest
-    pos_buf = be._positions
-    quest.prepare_step(seq_lens)
+    # per-kernel durations of the layer step's two launches (score + select, attention),
+    # each from a graph of L launches at the same shapes, HIP events on the launch stream
+    torch.add(base, seq_lens - 1, out=out_loc)
+    be.quest.prepare_step(seq_lens)
 
     def score_select():
-        quest.retrieve_topk(q_all[0], 0, rpi, seq_lens, out=pos_buf)
+        be.forward_decode_phase(q_all[0], k_new[0], v_new[0], layers[0], batch, 1)
 
     def attend():
-        be.sparse_attention(q_all[0], layers[0], rpi, pos_buf[:B], quest._step.actual_lens, B)
+        be.forward_decode_phase(q_all[0], k_new[0], v_new[0], layers[0], batch, 2)
 
     ms_sel = time_graph(score_select, L, stream)
     ms_att = time_graph(attend, L, stream)
     bw_sel = byts["bounds"] / (ms_sel * 1e-3) / 1e9
     bw_att = byts["kv"] / (ms_att * 1e-3) / 1e9
-    dominant = ("quest_decode_attention", ms_att, byts["kv"], bw_att) if ms_att >= ms_sel else (
-        "quest_score_select", ms_sel, byts["bounds"], bw_sel)
+    dominant = ("quest_attend_head_kernel", ms_att, byts["kv"], bw_att) if ms_att >= ms_sel else (
+        "quest_score_select_kernel", ms_sel, byts["bounds"], bw_sel)
 
     cpu = None
     if args.cpu_sample > 0:
@@ -221,8 +221,8 @@ def main() -> int:
         "hbm_frac_layer_step": round(step_frac, 4),
         "tokens_per_s": round(B / (ms_per_step * 1e-3), 1),
         "algorithmic_bytes_per_layer_step": byts,
-        "kernels_us": {"quest_score_select": round(ms_sel * 1e3, 2),
-                       "quest_decode_attention": round(ms_att * 1e3, 2)},
+        "kernels_us": {"quest_score_select_kernel": round(ms_sel * 1e3, 2),
+                       "quest_attend_head_kernel": round(ms_att * 1e3, 2)},
         "roofline": {"kernel": dominant[0], "bound": "hbm", "achieved": round(dominant[3], 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(dominant[3] / HBM_PEAK_GBS, 4),
                      "traffic": None},

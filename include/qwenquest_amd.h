@@ -197,6 +197,25 @@ int qq_quest_forward_decode(const void* q, int q_dtype, int64_t q_batch_stride, 
                             float* scores_ws, int32_t* positions, void* out, void* workspace,
                             int64_t workspace_bytes, void* sync, int64_t sync_bytes, void* stream);
 
+/* qq_quest_forward_decode split into its two stages, for callers that run
+ * other work between them or time them separately: phase 1 = scoring +
+ * selection and the new token's K/V store, phase 2 = layout + attention
+ * (consumes what phase 1 left in `workspace` / `positions`), phase 3 = both.
+ * `positions` and `out` are complete after phase 2.  Arguments as for
+ * qq_quest_forward_decode; no counterpart in the reference. */
+int qq_quest_forward_decode_phase(const void* q, int q_dtype, int64_t q_batch_stride, int num_q_heads,
+                                  const void* k_new, const void* v_new, int new_dtype,
+                                  const int64_t* out_cache_loc, void* k_layer, void* v_layer,
+                                  int kv_dtype, int64_t kv_rows, const uint16_t* page_k_bounds,
+                                  int layer, const int64_t* req_pool_indices, const int64_t* seq_lens,
+                                  const int32_t* candidate_limit, const int32_t* actual_lens, int bs,
+                                  int max_reqs, int max_pages, int kv_heads, int head_dim,
+                                  int page_size, int top_k, const int32_t* req_to_token,
+                                  int64_t req_to_token_stride, int64_t req_to_token_rows, float scale,
+                                  float* scores_ws, int32_t* positions, void* out, void* workspace,
+                                  int64_t workspace_bytes, void* sync, int64_t sync_bytes, int phase,
+                                  void* stream);
+
 /* Replaces MHATokenToKVPool.set_kv_buffer (src/qwenquest/memory.py:114-120):
  * k_layer[locs[i]] = k[i], v_layer[locs[i]] = v[i] (row = KV*D elements),
  * converting src_dtype -> buf_dtype. */

@@ -111,6 +111,12 @@ class QuestOnlyBackend(AttentionBackend):
 
     def forward_decode(self, q, k, v, layer, batch: ForwardBatch) -> torch.Tensor:
         """quest_only.py:132-159 in one C call: save the new K/V, select, gather + attend."""
+        return self.forward_decode_phase(q, k, v, layer, batch, 3)
+
+    def forward_decode_phase(self, q, k, v, layer, batch: ForwardBatch, phase: int) -> torch.Tensor:
+        """forward_decode's stages: 1 = scoring + selection + new-token store, 2 = layout +
+        attention (after phase 1 of the same layer and batch), 3 = both.  Returns the output
+        tensor (complete after phase 2)."""
         assert batch.out_cache_loc is not None
         quest = self.quest
         step = quest._step
@@ -139,7 +145,7 @@ class QuestOnlyBackend(AttentionBackend):
         r2t = self.req_to_token
         sync = self._step_sync  # None: the four-launch path
         _lib.call(
-            "qq_quest_forward_decode", _lib.ptr(q3), _lib.dtype_code(q3.dtype), q3.stride(0), heads,
+            "qq_quest_forward_decode_phase", _lib.ptr(q3), _lib.dtype_code(q3.dtype), q3.stride(0), heads,
             _lib.ptr(kn), _lib.ptr(vn), _lib.dtype_code(kn.dtype), _lib.ptr(loc), _lib.ptr(k_buf),
             _lib.ptr(v_buf), _lib.dtype_code(k_buf.dtype), k_buf.shape[0], _lib.ptr(quest.page_k_bounds),
             layer.layer_id - quest.start_layer, _lib.ptr(rpi), _lib.ptr(step.seq_lens),
@@ -147,9 +153,9 @@ class QuestOnlyBackend(AttentionBackend):
             quest.max_pages_per_req, quest.kv_heads, quest.head_dim, quest.page_size, quest.top_k,
             _lib.ptr(r2t), r2t.stride(0), r2t.shape[0], float(layer.scaling), _lib.ptr(quest._scores_ws),
             _lib.ptr(self._positions), _lib.ptr(out), _lib.ptr(buf), buf.numel(), _lib.ptr(sync),
-            0 if sync is None else sync.numel(), _lib.stream(q3.device),
+            0 if sync is None else sync.numel(), int(phase), _lib.stream(q3.device),
         )
-        if quest.trace is not None:
+        if quest.trace is not None and phase & 2:
             quest._record(layer.layer_id, rpi, step, self._positions[:bs])
         return out
 

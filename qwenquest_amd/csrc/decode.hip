@@ -3,24 +3,26 @@
 // token's K/V, select the positions, gather through req_to_token and attend.
 //
 // Fused path (bf16, KV*D = 4*128, page 64, at most 64 selected pages, at most
-// 4096 pages per request, and a zeroed sync buffer from the caller): two
-// launches, each small enough per block that the whole grid is resident at
-// once, so every block's chain of dependent memory round trips overlaps the
-// others' streaming:
-//   1. score + select, one block per (request, 32 candidate pages): 4 waves x
-//      8 pages scored, scores out with agent-scope stores, then the block
-//      counts itself on its request's counter.  The block that completes the
-//      count selects the request's pages (filter top-k over the scores) and
-//      writes the layout: positions [bs, top_k], the pool rows they map to
-//      through req_to_token (workspace), and the new token's K/V
-//      (set_kv_buffer, memory.py:114-120).
-//   2. attention + merge, one block per (request, 4 chunks of 64 layout rows,
-//      KV head): each wave attends one chunk with MFMA, the 4 waves combine in
-//      LDS into an (m, l, o) partial (agent-scope stores); the block that
-//      completes a (request, KV head) count merges the partials into the
-//      output.
+// 4096 pages per request, top_k <= 4096, and a zeroed sync buffer from the
+// caller): two launches.
+//   1. score + select, one block per (request, 32 candidate pages), the whole
+//      grid resident at once: 4 waves x 8 pages scored, scores out with
+//      agent-scope stores, then the block counts itself on its request's
+//      counter.  The block that completes the count selects the request's
+//      pages (filter top-k over the scores) and writes the page list, and
+//      stores the new token's K/V (set_kv_buffer, memory.py:114-120).
+//   2. attention, one block per (request, KV head, part of the rows), enough
+//      parts to put one block on every CU: the block turns its share of the
+//      page list into layout positions and pool rows (req_to_token,
+//      quest_only.py:149-151) in LDS - the KV-head-0 blocks also write the
+//      positions - then each of its 8 waves streams its rows in steps of 32
+//      with 2 steps in flight and an online softmax (MFMA QK^T and PV), and
+//      the waves combine in LDS.  The parts'
+//      (m, l, o) partials go out with agent-scope stores; the block that
+//      completes a (request, KV head) count merges them into the output.
 // The counters return to zero before each launch ends, so the next call (or a
-// graph replay) starts clean.
+// graph replay) starts clean.  A CU streams only ~30-40 GB/s of these 256-byte
+// row slices, so the attention grid covers every CU.
 //
 // Other shapes: four launches on one stream, each consuming the previous one's
 // output: score (all CUs) -> select + new-token store (one block per request)
@@ -35,7 +37,10 @@ constexpr int kStepM = 8;             // bounds words per lane (512 / 64)
 constexpr int kStepPagesPerTile = 32; // score tile: 4 waves x 8 pages
 constexpr int kStepMaxG = 16;
 constexpr int kMaxSelFused = 64;
-constexpr int kStepMaxNT = (kMaxSelFused + 1 + 3) / 4;  // 64-row chunks / 4 per tile
+constexpr int kStepMaxTopK = 4096;
+constexpr int kHeadWaves = 8;        // attention block: 8 waves (two per SIMD)
+constexpr int kHeadDepth = 2;        // steps of 32 rows in flight per wave
+constexpr int kMaxParts = 8;         // attention blocks per (request, KV head)
 
 struct StepArgs {
   SelectArgs s;            // scoring, selection, positions, new token
@@ -46,17 +51,18 @@ struct StepArgs {
   int64_t r2t_stride, r2t_rows;
   float sl2;               // scale * log2(e)
   uint16_t* out;           // [bs, H * 128] bf16
-  float* part_o;           // [bs, KV, NT, G, 128]
-  float* part_ml;          // [bs, KV, NT, G, 2] (m in log2 units, l)
-  int32_t* rows;           // [bs, top_k] pool rows of the layout
+  int32_t* pages;          // [bs, 64] selected pages by rank (workspace)
+  float* part_o;           // [bs, KV, parts, G, 128] attention partials (workspace)
+  float* part_ml;          // [bs, KV, parts, G, 2] (m in log2 units, l)
   uint32_t* sync;
-  int bs, tiles_s, nt, G;
+  int bs, tiles_s, G;
+  int parts, per_wave;     // attention blocks per (request, KV head); rows per wave
 };
 
-// sync layout (uint32 words, each counter on its own 128-byte line):
-//   score count [bs], attention count [KV][bs].
+// sync (uint32 words, each counter on its own 128-byte line): score count [bs],
+// attention count [bs * KV].
 __device__ inline uint32_t* score_count(const StepArgs& a, int b) { return a.sync + b * 32; }
-__device__ inline uint32_t* attn_count(const StepArgs& a, int b, int h) { return a.sync + ((1 + h) * a.bs + b) * 32; }
+__device__ inline uint32_t* attn_count(const StepArgs& a, int bh) { return a.sync + (a.bs + bh) * 32; }
 
 __device__ inline bool needs_selection(const SelectArgs& sa, int64_t s) { return s > sa.top_k && sa.k_sel > 0; }
 
@@ -66,26 +72,24 @@ union ScoreSmem {
   SelectSmem<KPT> sel;
 };
 
-// The request's selection and layout (quest.py:409-464), run by the block
-// that completed its score count: positions, pool rows (quest_only.py:149-151)
-// and the new token's K/V (C = 512 bf16 = 256 words per row).
+// The request's selection (quest.py:409-464), run by the block that completed
+// its score count: the top-k pages by rank into the page list, and the new
+// token's K/V (C = 512 bf16 = 256 words per row).
 template <int KPT>
 __device__ void select_request(const StepArgs& a, int b, ScoreSmem<KPT>& sm) {
   const SelectArgs& sa = a.s;
   const int tid = threadIdx.x;
   const int64_t s = sa.seq[b];
   const int64_t req = sa.rpi[b];
-  const bool req_ok = req >= 0 && req < sa.R;
-  const int lim = req_ok ? min(sa.limit[b], sa.MP) : 0;
-  const int k = sa.k_sel, P = sa.P, top_k = sa.top_k;
-  const bool long_b = needs_selection(sa, s);
+  const int lim = (req >= 0 && req < sa.R) ? min(sa.limit[b], sa.MP) : 0;
+  const int k = sa.k_sel;
   const int64_t loc = sa.new_k ? sa.new_locs[b] : -1;
   uint32_t kw = 0u, vw = 0u;
   if (sa.new_k) {
     kw = static_cast<const uint32_t*>(sa.new_k)[(int64_t)b * 256 + tid];
     vw = static_cast<const uint32_t*>(sa.new_v)[(int64_t)b * 256 + tid];
   }
-  if (long_b) {
+  if (needs_selection(sa, s)) {
     const float* sc = sa.scores + (int64_t)b * sa.MP;
     float sv[KPT];
 #pragma unroll
@@ -94,36 +98,7 @@ __device__ void select_request(const StepArgs& a, int b, ScoreSmem<KPT>& sm) {
       sv[i] = p < lim ? ld_agent(sc + p) : 0.0f;
     }
     select_topk_block<KPT>(sv, lim, max(lim, k), k, sm.sel);
-  }
-  // layout slot -> position (pages by rank, then the recent window; or dense)
-  int32_t* pos = sa.positions + (int64_t)b * top_k;
-  int32_t* rows = a.rows + (int64_t)b * top_k;
-  const bool r2t_ok = req >= 0 && req < a.r2t_rows;
-  for (int slot0 = 0; slot0 < top_k; slot0 += kBlock * 8) {
-    int64_t pv[8];
-    int32_t rv[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int slot = slot0 + tid + kBlock * i;
-      int64_t p;
-      if (!long_b)
-        p = s <= top_k ? min((int64_t)slot, max(s - 1, (int64_t)0)) : min(max(s - P, (int64_t)0) + slot, s - 1);
-      else if (slot < k * P)
-        p = (int64_t)sm.sel.order[slot / P] * P + slot % P;
-      else
-        p = min(max(s - P, (int64_t)0) + (slot - k * P), s - 1);
-      pv[i] = p;
-      rv[i] = (slot < top_k && r2t_ok && p >= 0 && p < a.r2t_stride) ? a.r2t[req * a.r2t_stride + p] : 0;
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int slot = slot0 + tid + kBlock * i;
-      if (slot < top_k) {
-        pos[slot] = (int32_t)pv[i];
-        const int64_t row = rv[i];
-        rows[slot] = (row >= 0 && row < a.kv_rows) ? (int32_t)row : 0;
-      }
-    }
+    if (tid < k) a.pages[b * kMaxSelFused + tid] = sm.sel.order[tid];
   }
   if (loc >= 0 && loc < sa.pool_rows) {
     static_cast<uint32_t*>(sa.k_pool)[loc * 256 + tid] = kw;
@@ -165,43 +140,199 @@ __global__ __launch_bounds__(kBlock) void quest_score_select_kernel(StepArgs a) 
   select_request<KPT>(a, b, sm);
 }
 
-struct AttnSmem {
-  const uint16_t* kp[kBlockWaves][64];
-  const uint16_t* vp[kBlockWaves][64];
-  float m[kBlockWaves][kStepMaxG];
-  float l[kBlockWaves][kStepMaxG];
-  float o[kBlockWaves][kStepMaxG][kMfmaDim];
+// One wave's step: the K and V slices of 32 layout rows of one KV head
+// (lane layouts of attn_wave64: K tile t = tokens 16t .. 16t+15, V k-step u =
+// tokens 16u .. 16u+15).
+struct StepRegs {
+  bf16x8_t ka[2][4];
+  uint4 vr[2][4];
 };
 
-__global__ __launch_bounds__(kBlock) void quest_attend_merge_kernel(StepArgs a) {
-  __shared__ AttnSmem sm_attn;
+__device__ inline void load_step(StepRegs& r, const int32_t* rows, int t0, const uint16_t* kb, const uint16_t* vb,
+                                 int lo, int hi) {
+  constexpr int kRow = kStepKV * kMfmaDim;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const uint16_t* kp = kb + (int64_t)rows[t0 + t * 16 + lo] * kRow + hi * 8;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) r.ka[t][ks] = *reinterpret_cast<const bf16x8_t*>(kp + ks * 32);
+  }
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      r.vr[u][j] = *reinterpret_cast<const uint4*>(vb + (int64_t)rows[t0 + u * 16 + hi * 4 + j] * kRow + lo * 8);
+}
+
+// Online-softmax update with one step (tokens t0 .. t0+31, the first `valid`
+// of them real): M, L per head lo (log2 units), o[e][i] per (head 4hi+i,
+// channel 8lo+e).
+__device__ inline void attend_step(const StepRegs& r, const bf16x8_t (&qb)[4], int valid, float sl2, float& M,
+                                   float& L, float4_t (&o)[8], int lo, int hi) {
+  float4_t acc[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    acc[t] = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(r.ka[t][ks], qb[ks], acc[t], 0, 0, 0);
+  }
+  float mx = -INFINITY;
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float x = (t * 16 + hi * 4 + i) < valid ? acc[t][i] * sl2 : -INFINITY;
+      acc[t][i] = x;
+      mx = fmaxf(mx, x);
+    }
+  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  const float Mn = fmaxf(M, mx);
+  const float alpha = M == -INFINITY ? 0.0f : exp2f(M - Mn);  // rescale of the running sums
+  float sum = 0.0f;
+  short4_t pa[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint16_t pb = Mn == -INFINITY ? (uint16_t)0 : f2bf(exp2f(acc[t][i] - Mn));
+      sum += bf2f(pb);
+      pa[t][i] = (short)pb;
+    }
+  sum += __shfl_xor(sum, 16, 64);
+  sum += __shfl_xor(sum, 32, 64);
+  L = L * alpha + sum;
+  M = Mn;
+  // o rows are heads 4hi + i: their scale factors live in lanes 4hi + i
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float ai = __shfl(alpha, hi * 4 + i, 64);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e][i] *= ai;
+  }
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    short4_t vbv[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint4 w = r.vr[u][j];
+      const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int x = 0; x < 4; ++x) {
+        vbv[2 * x][j] = (short)(wv[x] & 0xFFFFu);
+        vbv[2 * x + 1][j] = (short)(wv[x] >> 16);
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa[u], vbv[e], o[e], 0, 0, 0);
+  }
+}
+
+struct HeadSmem {
+  int32_t rows[kStepMaxTopK];  // this block's layout slots -> pool rows
+  float m[kHeadWaves][kStepMaxG];
+  float l[kHeadWaves][kStepMaxG];
+  float o[kHeadWaves][kStepMaxG][kMfmaDim];
+};
+
+// Attention of one (request, KV head, part): the block's share of the layout
+// slots, per_wave rows per wave in steps of 32 (kHeadDepth in flight), the
+// waves combined in LDS.  With one part the block writes the output; else it
+// stores an (m, l, o) partial (agent scope) and the block that completes the
+// (request, KV head) count merges the parts.
+__global__ __launch_bounds__(64 * kHeadWaves, 1) void quest_attend_part_kernel(StepArgs a) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  HeadSmem& sm = *reinterpret_cast<HeadSmem*>(smem_raw);
   __shared__ uint32_t s_last;
   const SelectArgs& sa = a.s;
+  constexpr int kThreads = 64 * kHeadWaves;
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
-  const int per_req = kStepKV * a.nt;
-  const int b = blockIdx.x / per_req, rem = blockIdx.x - b * per_req;
-  const int j = rem / kStepKV, h = rem - j * kStepKV;  // the 4 heads of a row block are adjacent
+  const int lo = lane & 15, hi = lane >> 4;
+  const int parts = a.parts;
+  const int bh = blockIdx.x / parts, part = blockIdx.x - bh * parts;
+  const int b = bh / kStepKV, h = bh - b * kStepKV;
   const int64_t s = sa.seq[b];
-  const int n = (int)min(max(s, (int64_t)0), (int64_t)sa.top_k);  // actual_lens (quest.py:345)
-  const int c = j * kBlockWaves + wave;  // this wave's chunk of 64 layout slots
-  const int cnt = max(0, min(64, n - c * 64));
+  const int64_t req = sa.rpi[b];
+  const int top_k = sa.top_k, P = sa.P, k = sa.k_sel;
+  const bool long_b = needs_selection(sa, s);
+  const int n = (int)min(max(s, (int64_t)0), (int64_t)top_k);  // actual_lens (quest.py:345)
+  const bool r2t_ok = req >= 0 && req < a.r2t_rows;
+  // slots [slot_base, slot_base + per_block): per_wave rows per wave, a multiple of
+  // the 32-row step; the row table is filled over the whole range (row 0 past n),
+  // so every row a step reads is initialised and in range
+  const int per_wave = a.per_wave;
+  const int per_block = kHeadWaves * per_wave;  // <= kStepMaxTopK
+  const int slot_base = part * per_block;
+  int32_t* pos_out = h == 0 ? sa.positions + (int64_t)b * top_k : nullptr;
+  for (int i0 = 0; i0 < per_block; i0 += kThreads * 4) {
+    int64_t pv[4];
+    int32_t rv[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int slot = slot_base + i0 + tid + kThreads * u;
+      int64_t p;
+      if (!long_b)
+        p = s <= top_k ? min((int64_t)slot, max(s - 1, (int64_t)0)) : min(max(s - P, (int64_t)0) + slot, s - 1);
+      else if (slot < k * P)
+        p = (int64_t)a.pages[b * kMaxSelFused + slot / P] * P + slot % P;
+      else
+        p = min(max(s - P, (int64_t)0) + (slot - k * P), s - 1);
+      pv[u] = p;
+      rv[u] = (slot < n && r2t_ok && p >= 0 && p < a.r2t_stride) ? a.r2t[req * a.r2t_stride + p] : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int i = i0 + tid + kThreads * u;
+      const int slot = slot_base + i;
+      if (i < per_block) {
+        const int64_t row = rv[u];
+        sm.rows[i] = (slot < n && row >= 0 && row < a.kv_rows) ? (int32_t)row : 0;
+        if (pos_out && slot < top_k) pos_out[slot] = (int32_t)pv[u];
+      }
+    }
+  }
+  const int G = a.G;
+  bf16x8_t qb[4];
   {
-    constexpr int kRow = kStepKV * kMfmaDim;
-    const int64_t row = lane < cnt ? a.rows[(int64_t)b * sa.top_k + c * 64 + lane] : 0;
-    sm_attn.kp[wave][lane] = a.k + row * kRow + h * kMfmaDim;
-    sm_attn.vp[wave][lane] = a.v + row * kRow + h * kMfmaDim;
+    const uint16_t* qp = static_cast<const uint16_t*>(sa.q) + (int64_t)b * sa.q_bstride +
+                         (int64_t)(h * G + lo) * kMfmaDim + hi * 8;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      if (lo < G) {
+        qb[ks] = *reinterpret_cast<const bf16x8_t*>(qp + ks * 32);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qb[ks][e] = (__bf16)0.0f;
+      }
+    }
   }
   __syncthreads();
-  const int G = a.G;
-  const int lo = lane & 15, hi = lane >> 4;
-  float mx, sum;
+  // this wave's rows: local [r0, r0 + per_wave), real up to slot n
+  const int r0 = wave * per_wave;
+  const int r_end = max(r0, min(r0 + per_wave, n - slot_base));
+  const int nsteps = (r_end - r0 + 31) / 32;
+  const uint16_t* kb = a.k + h * kMfmaDim;
+  const uint16_t* vb = a.v + h * kMfmaDim;
+  float M = -INFINITY, L = 0.0f;
   float4_t o[8];
-  const uint16_t* qh =
-      static_cast<const uint16_t*>(sa.q) + (int64_t)b * sa.q_bstride + (int64_t)h * G * kMfmaDim;
-  AttnSmem& sm = sm_attn;
-  attn_wave64(sm.kp[wave], sm.vp[wave], qh, G, cnt, a.sl2, mx, sum, o);
-  // combine the 4 waves' chunks in LDS
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = float4_t{0.f, 0.f, 0.f, 0.f};
+  StepRegs ring[kHeadDepth];
+#pragma unroll
+  for (int j = 0; j < kHeadDepth - 1; ++j)
+    if (j < nsteps) load_step(ring[j], sm.rows, r0 + 32 * j, kb, vb, lo, hi);
+  for (int i0 = 0; i0 < nsteps; i0 += kHeadDepth) {
+#pragma unroll
+    for (int j = 0; j < kHeadDepth; ++j) {
+      const int i = i0 + j;
+      if (i >= nsteps) break;
+      const int ahead = i + kHeadDepth - 1;
+      if (ahead < nsteps) load_step(ring[(j + kHeadDepth - 1) % kHeadDepth], sm.rows, r0 + 32 * ahead, kb, vb, lo, hi);
+      attend_step(ring[j], qb, r_end - (r0 + 32 * i), a.sl2, M, L, o, lo, hi);
+    }
+  }
+  // combine the waves in LDS
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int head = hi * 4 + i;
@@ -212,80 +343,80 @@ __global__ __launch_bounds__(kBlock) void quest_attend_merge_kernel(StepArgs a) 
     }
   }
   if (hi == 0 && lo < G) {
-    sm.m[wave][lo] = mx;
-    sm.l[wave][lo] = sum;
+    sm.m[wave][lo] = M;
+    sm.l[wave][lo] = L;
   }
   __syncthreads();
-  const int64_t part = ((int64_t)b * kStepKV + h) * a.nt + j;
-#pragma unroll
-  for (int r = 0; r < kStepMaxG * kMfmaDim / kBlock; ++r) {
-    const int idx = tid + kBlock * r;
+  uint16_t* outp = a.out + (int64_t)b * sa.H * kMfmaDim + (int64_t)h * G * kMfmaDim;
+  const int64_t part_idx = (int64_t)bh * parts + part;
+  for (int idx = tid; idx < G * kMfmaDim; idx += kThreads) {
     const int head = idx >> 7, d = idx & 127;
-    if (head < G) {
-      float M = -INFINITY;
+    float Mx = -INFINITY;
 #pragma unroll
-      for (int w = 0; w < kBlockWaves; ++w) M = fmaxf(M, sm.m[w][head]);
-      float L = 0.0f, O = 0.0f;
+    for (int w = 0; w < kHeadWaves; ++w) Mx = fmaxf(Mx, sm.m[w][head]);
+    float Ls = 0.0f, Os = 0.0f;
 #pragma unroll
-      for (int w = 0; w < kBlockWaves; ++w) {
-        const float mw = sm.m[w][head];
-        const float wgt = mw == -INFINITY ? 0.0f : exp2f(mw - M);
-        L += wgt * sm.l[w][head];
-        O += wgt * sm.o[w][head][d];
-      }
-      st_agent(a.part_o + (part * G + head) * kMfmaDim + d, O);
+    for (int w = 0; w < kHeadWaves; ++w) {
+      const float mw = sm.m[w][head];
+      const float wgt = mw == -INFINITY ? 0.0f : exp2f(mw - Mx);
+      Ls += wgt * sm.l[w][head];
+      Os += wgt * sm.o[w][head][d];
+    }
+    if (parts == 1) {
+      outp[idx] = f2bf(Ls > 0.0f ? Os / Ls : 0.0f);
+    } else {
+      st_agent(a.part_o + (part_idx * G + head) * kMfmaDim + d, Os);
       if (d == 0) {
-        st_agent(a.part_ml + (part * G + head) * 2, M);
-        st_agent(a.part_ml + (part * G + head) * 2 + 1, L);
+        st_agent(a.part_ml + (part_idx * G + head) * 2, Mx);
+        st_agent(a.part_ml + (part_idx * G + head) * 2 + 1, Ls);
       }
     }
   }
+  if (parts == 1) return;
   wait_memory();
   __syncthreads();
-  if (tid == 0) s_last = add_agent(attn_count(a, b, h), 1u) == (uint32_t)(a.nt - 1);
+  if (tid == 0) s_last = add_agent(attn_count(a, bh), 1u) == (uint32_t)(parts - 1);
   __syncthreads();
   if (!s_last) return;
-  if (tid == 0) st_agent(attn_count(a, b, h), 0u);
-  // merge the NT partials of (request b, KV head h) into the output: each
-  // thread one head x 4 channels, all of its partial loads in flight at once
-  const int64_t part0 = ((int64_t)b * kStepKV + h) * a.nt;
+  if (tid == 0) st_agent(attn_count(a, bh), 0u);
+  // merge the parts: each thread one head x 4 channels, all loads in flight at once
+  const int64_t part0 = (int64_t)bh * parts;
   const __amdgpu_buffer_rsrc_t ro =
-      agent_rsrc(a.part_o + part0 * G * kMfmaDim, (uint32_t)(a.nt * G * kMfmaDim * sizeof(float)));
+      agent_rsrc(a.part_o + part0 * G * kMfmaDim, (uint32_t)(parts * G * kMfmaDim * sizeof(float)));
   const uint64_t* ml64 = reinterpret_cast<const uint64_t*>(a.part_ml) + part0 * G;
-  for (int grp = tid; grp < G * (kMfmaDim / 4); grp += kBlock) {
+  for (int grp = tid; grp < G * (kMfmaDim / 4); grp += kThreads) {
     const int head = grp >> 5, d4 = (grp & 31) * 4;
-    float4 ov[kStepMaxNT];
-    uint64_t mlv[kStepMaxNT];
+    float4 ov[kMaxParts];
+    uint64_t mlv[kMaxParts];
 #pragma unroll
-    for (int jj = 0; jj < kStepMaxNT; ++jj) {
-      if (jj < a.nt) {
-        ov[jj] = ld_agent_x4(ro, (uint32_t)(((jj * G + head) * kMfmaDim + d4) * sizeof(float)));
-        mlv[jj] = ld_agent(ml64 + jj * G + head);
+    for (int j = 0; j < kMaxParts; ++j) {
+      if (j < parts) {
+        ov[j] = ld_agent_x4(ro, (uint32_t)(((j * G + head) * kMfmaDim + d4) * sizeof(float)));
+        mlv[j] = ld_agent(ml64 + j * G + head);
       }
     }
-    float M = -INFINITY;
+    float Mx = -INFINITY;
 #pragma unroll
-    for (int jj = 0; jj < kStepMaxNT; ++jj)
-      if (jj < a.nt) M = fmaxf(M, __uint_as_float((uint32_t)mlv[jj]));
-    float L = 0.0f;
-    float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int j = 0; j < kMaxParts; ++j)
+      if (j < parts) Mx = fmaxf(Mx, __uint_as_float((uint32_t)mlv[j]));
+    float Ls = 0.0f;
+    float4 Os = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-    for (int jj = 0; jj < kStepMaxNT; ++jj) {
-      if (jj < a.nt) {
-        const float mj = __uint_as_float((uint32_t)mlv[jj]);
-        const float wgt = mj == -INFINITY ? 0.0f : exp2f(mj - M);
-        L += wgt * __uint_as_float((uint32_t)(mlv[jj] >> 32));
-        O.x += wgt * ov[jj].x;
-        O.y += wgt * ov[jj].y;
-        O.z += wgt * ov[jj].z;
-        O.w += wgt * ov[jj].w;
+    for (int j = 0; j < kMaxParts; ++j) {
+      if (j < parts) {
+        const float mj = __uint_as_float((uint32_t)mlv[j]);
+        const float wgt = mj == -INFINITY ? 0.0f : exp2f(mj - Mx);
+        Ls += wgt * __uint_as_float((uint32_t)(mlv[j] >> 32));
+        Os.x += wgt * ov[j].x;
+        Os.y += wgt * ov[j].y;
+        Os.z += wgt * ov[j].z;
+        Os.w += wgt * ov[j].w;
       }
     }
-    uint16_t* dst = a.out + (int64_t)b * sa.H * kMfmaDim + (int64_t)(h * G + head) * kMfmaDim + d4;
-    const bool any = L > 0.0f;
-    const uint32_t lo2 = (uint32_t)f2bf(any ? O.x / L : 0.0f) | ((uint32_t)f2bf(any ? O.y / L : 0.0f) << 16);
-    const uint32_t hi2 = (uint32_t)f2bf(any ? O.z / L : 0.0f) | ((uint32_t)f2bf(any ? O.w / L : 0.0f) << 16);
-    *reinterpret_cast<uint2*>(dst) = make_uint2(lo2, hi2);
+    const bool any = Ls > 0.0f;
+    const uint32_t lo2 = (uint32_t)f2bf(any ? Os.x / Ls : 0.0f) | ((uint32_t)f2bf(any ? Os.y / Ls : 0.0f) << 16);
+    const uint32_t hi2 = (uint32_t)f2bf(any ? Os.z / Ls : 0.0f) | ((uint32_t)f2bf(any ? Os.w / Ls : 0.0f) << 16);
+    *reinterpret_cast<uint2*>(outp + head * kMfmaDim + d4) = make_uint2(lo2, hi2);
   }
 }
 
@@ -296,10 +427,35 @@ using namespace qq;
 
 extern "C" int64_t qq_quest_layer_step_sync_bytes(int bs, int kv_heads) {
   if (bs <= 0 || kv_heads <= 0) return 0;
-  return (int64_t)(1 + kStepKV) * bs * 32 * (int64_t)sizeof(uint32_t);
+  return (int64_t)bs * (1 + kv_heads) * 32 * (int64_t)sizeof(uint32_t);
 }
 
-extern "C" int qq_quest_forward_decode(
+// Compute units of the current device (cached per device).
+static int device_cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+// LDS of the attention kernel (above the 64 KiB default: opted in once per device).
+static size_t head_smem_bytes() {
+  static bool opted[64] = {false};
+  int dev = 0;
+  if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64 && !opted[dev]) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&quest_attend_part_kernel),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)sizeof(HeadSmem));
+    opted[dev] = true;
+  }
+  return sizeof(HeadSmem);
+}
+
+static int forward_decode(
     const void* q, int q_dtype, int64_t q_batch_stride, int num_q_heads, const void* k_new,
     const void* v_new, int new_dtype, const int64_t* out_cache_loc, void* k_layer, void* v_layer,
     int kv_dtype, int64_t kv_rows, const uint16_t* page_k_bounds, int layer,
@@ -307,8 +463,7 @@ extern "C" int qq_quest_forward_decode(
     const int32_t* actual_lens, int bs, int max_reqs, int max_pages, int kv_heads, int head_dim,
     int page_size, int top_k, const int32_t* req_to_token, int64_t req_to_token_stride,
     int64_t req_to_token_rows, float scale, float* scores_ws, int32_t* positions, void* out,
-    void* workspace, int64_t workspace_bytes, void* sync, int64_t sync_bytes, void* stream) {
-  const char* what = "qq_quest_forward_decode";
+    void* workspace, int64_t workspace_bytes, void* sync, int64_t sync_bytes, int phase, hipStream_t s, const char* what) {
   QQ_REQUIRE(dtype_ok(q_dtype) && dtype_ok(kv_dtype) && dtype_ok(new_dtype), "%s: unsupported dtype",
              what);
   QQ_REQUIRE(kv_heads > 0 && head_dim > 0 && num_q_heads > 0 && num_q_heads % kv_heads == 0,
@@ -324,8 +479,8 @@ extern "C" int qq_quest_forward_decode(
                  candidate_limit && actual_lens && req_to_token && scores_ws && positions && out,
              "%s: null pointer", what);
   QQ_REQUIRE(!k_new || (v_new && out_cache_loc), "%s: new K without V or locations", what);
+  QQ_REQUIRE(phase >= 1 && phase <= 3, "%s: phase %d is not 1, 2 or 3", what, phase);
   if (bs == 0) return QQ_OK;
-  hipStream_t s = static_cast<hipStream_t>(stream);
 
   SelectArgs sa;
   sa.q = q;
@@ -359,15 +514,19 @@ extern "C" int qq_quest_forward_decode(
   sa.pool_rows = kv_rows;
 
   const int G = num_q_heads / kv_heads;
-  const int chunks = top_k / page_size;
-  const int nt = ceil_div(chunks, kBlockWaves);
-  const int64_t part_bytes = (int64_t)bs * kStepKV * nt * G * (kMfmaDim + 2) * (int64_t)sizeof(float);
-  const int64_t rows_bytes = (int64_t)bs * top_k * (int64_t)sizeof(int32_t);
+  const int64_t pages_bytes = (int64_t)bs * kMaxSelFused * (int64_t)sizeof(int32_t);
+  // attention blocks per (request, KV head): enough to cover every CU once (the
+  // blocks run one per CU), at least 32 rows per wave
+  const int parts = max(1, min(kMaxParts, min(device_cu_count() / max(1, bs * kv_heads),
+                                              ceil_div(top_k, kHeadWaves * 32))));
+  const int per_wave = ceil_div(top_k, parts * kHeadWaves * 32) * 32;
+  const int64_t part_bytes = (int64_t)bs * kv_heads * parts * G * (kMfmaDim + 2) * (int64_t)sizeof(float);
   const bool fused = sync && sync_bytes >= qq_quest_layer_step_sync_bytes(bs, kv_heads) &&
                      q_dtype == QQ_DTYPE_BF16 && kv_dtype == QQ_DTYPE_BF16 &&
                      (!k_new || new_dtype == QQ_DTYPE_BF16) && kv_heads == kStepKV &&
                      head_dim == kMfmaDim && G <= kStepMaxG && page_size == 64 && k_sel <= kMaxSelFused &&
-                     max_pages <= 16 * kBlock && workspace && workspace_bytes >= part_bytes + rows_bytes;
+                     top_k <= kStepMaxTopK && max_pages <= 16 * kBlock && workspace &&
+                     workspace_bytes >= pages_bytes + (parts > 1 ? part_bytes : 0);
   if (fused) {
     StepArgs a;
     a.s = sa;
@@ -379,17 +538,20 @@ extern "C" int qq_quest_forward_decode(
     a.r2t_rows = req_to_token_rows;
     a.sl2 = scale * kLog2e;
     a.out = static_cast<uint16_t*>(out);
-    a.part_o = static_cast<float*>(workspace);
-    a.part_ml = a.part_o + (int64_t)bs * kStepKV * nt * G * kMfmaDim;
-    a.rows = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + part_bytes);
+    a.pages = static_cast<int32_t*>(workspace);
+    a.part_o = reinterpret_cast<float*>(static_cast<char*>(workspace) + pages_bytes);
+    a.part_ml = a.part_o + (int64_t)bs * kv_heads * parts * G * kMfmaDim;
+    a.parts = parts;
+    a.per_wave = per_wave;
     a.sync = static_cast<uint32_t*>(sync);
     a.bs = bs;
     a.tiles_s = ceil_div(max(max_pages, 1), kStepPagesPerTile);
-    a.nt = nt;
     a.G = G;
     const int score_blocks = bs * a.tiles_s;
     const int n_max = max(max_pages, k_sel);
-    if (n_max <= 4 * kBlock)
+    if (!(phase & 1))
+      ;
+    else if (n_max <= 4 * kBlock)
       quest_score_select_kernel<4><<<score_blocks, kBlock, 0, s>>>(a);
     else if (n_max <= 8 * kBlock)
       quest_score_select_kernel<8><<<score_blocks, kBlock, 0, s>>>(a);
@@ -397,12 +559,14 @@ extern "C" int qq_quest_forward_decode(
       quest_score_select_kernel<12><<<score_blocks, kBlock, 0, s>>>(a);
     else
       quest_score_select_kernel<16><<<score_blocks, kBlock, 0, s>>>(a);
-    quest_attend_merge_kernel<<<bs * kStepKV * nt, kBlock, 0, s>>>(a);
+    if (phase & 2) quest_attend_part_kernel<<<bs * kStepKV * parts, 64 * kHeadWaves, head_smem_bytes(), s>>>(a);
     return check_launch(what);
   }
 
-  int st = launch_retrieve(sa, bs, s);
-  if (st != QQ_OK) return st;
+  if (phase & 1) {
+    const int st = launch_retrieve(sa, bs, s);
+    if (st != QQ_OK || !(phase & 2)) return st;
+  }
 
   AttnArgs aa;
   aa.q = q;
@@ -425,4 +589,34 @@ extern "C" int qq_quest_forward_decode(
   aa.scale = scale;
   aa.out = out;
   return launch_attention(aa, kv_dtype, bs, workspace_bytes, workspace, s, what);
+}
+
+extern "C" int qq_quest_forward_decode(
+    const void* q, int q_dtype, int64_t q_batch_stride, int num_q_heads, const void* k_new,
+    const void* v_new, int new_dtype, const int64_t* out_cache_loc, void* k_layer, void* v_layer,
+    int kv_dtype, int64_t kv_rows, const uint16_t* page_k_bounds, int layer,
+    const int64_t* req_pool_indices, const int64_t* seq_lens, const int32_t* candidate_limit,
+    const int32_t* actual_lens, int bs, int max_reqs, int max_pages, int kv_heads, int head_dim,
+    int page_size, int top_k, const int32_t* req_to_token, int64_t req_to_token_stride,
+    int64_t req_to_token_rows, float scale, float* scores_ws, int32_t* positions, void* out,
+    void* workspace, int64_t workspace_bytes, void* sync, int64_t sync_bytes, void* stream) {
+  return forward_decode(q, q_dtype, q_batch_stride, num_q_heads, k_new, v_new, new_dtype, out_cache_loc, k_layer, v_layer,
+      kv_dtype, kv_rows, page_k_bounds, layer, req_pool_indices, seq_lens, candidate_limit, actual_lens, bs,
+      max_reqs, max_pages, kv_heads, head_dim, page_size, top_k, req_to_token, req_to_token_stride,
+      req_to_token_rows, scale, scores_ws, positions, out, workspace, workspace_bytes, sync, sync_bytes, 3, static_cast<hipStream_t>(stream), "qq_quest_forward_decode");
+}
+
+extern "C" int qq_quest_forward_decode_phase(
+    const void* q, int q_dtype, int64_t q_batch_stride, int num_q_heads, const void* k_new,
+    const void* v_new, int new_dtype, const int64_t* out_cache_loc, void* k_layer, void* v_layer,
+    int kv_dtype, int64_t kv_rows, const uint16_t* page_k_bounds, int layer,
+    const int64_t* req_pool_indices, const int64_t* seq_lens, const int32_t* candidate_limit,
+    const int32_t* actual_lens, int bs, int max_reqs, int max_pages, int kv_heads, int head_dim,
+    int page_size, int top_k, const int32_t* req_to_token, int64_t req_to_token_stride,
+    int64_t req_to_token_rows, float scale, float* scores_ws, int32_t* positions, void* out,
+    void* workspace, int64_t workspace_bytes, void* sync, int64_t sync_bytes, int phase, void* stream) {
+  return forward_decode(q, q_dtype, q_batch_stride, num_q_heads, k_new, v_new, new_dtype, out_cache_loc, k_layer, v_layer,
+      kv_dtype, kv_rows, page_k_bounds, layer, req_pool_indices, seq_lens, candidate_limit, actual_lens, bs,
+      max_reqs, max_pages, kv_heads, head_dim, page_size, top_k, req_to_token, req_to_token_stride,
+      req_to_token_rows, scale, scores_ws, positions, out, workspace, workspace_bytes, sync, sync_bytes, phase, static_cast<hipStream_t>(stream), "qq_quest_forward_decode_phase");
 }

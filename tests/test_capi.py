@@ -86,3 +86,19 @@ def test_library_has_no_host_fallback_symbols(lib):
     exported = set(re.findall(r"\b(qq_\w+)\b", out))
     assert exported == set(_declarations())
     assert ctypes.sizeof(ctypes.c_void_p) == 8
+
+
+def test_forward_decode_phase_is_validated_without_gpu(lib):
+    """A phase other than 1, 2 or 3 is refused (QQ_EINVAL) before any HIP call; the
+    fused layer step's sync buffer holds one 128-byte counter line per request and one
+    per (request, KV head)."""
+    from qwenquest_amd import _lib
+
+    fake = ctypes.c_void_p(16)  # never dereferenced: validation fails first
+    args = [fake, 0, 4096, 32, None, None, 0, None, fake, fake, 0, 100, fake, 0, fake, fake, fake, fake,
+            2, 4, 64, 4, 128, 64, 2048, fake, 64, 4, 0.088, fake, fake, fake, fake, 1 << 20, None, 0]
+    for phase in (0, 4, -1):
+        st = lib.qq_quest_forward_decode_phase(*args, phase, None)
+        assert st == _lib.QQ_EINVAL and b"phase" in lib.qq_last_error()
+    assert lib.qq_quest_layer_step_sync_bytes(16, 4) == 16 * (1 + 4) * 128
+    assert lib.qq_quest_layer_step_sync_bytes(0, 4) == 0
