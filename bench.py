@@ -7,11 +7,13 @@ K/V pools (about 192 GiB) and page bounds (3 GiB) resident in HBM, inputs
 synthetic N(0, 1) from fixed seeds.
 
 One step = one decode step of all 48 layers through the drop-in backend:
-bounds append (fused over layers) + per layer: new K/V write, GQA-mean page
-scoring + top-31 selection + layout, req_to_token gather + split-K attention.
-The step is captured once in a HIP graph and replayed; seq_lens advance by one
-token per replay, so pages complete and get finalized during the run.
-Reported value: microseconds per layer-step (step time / 48).
+bounds append (fused over layers) + per layer two launches: GQA-mean page
+scoring + per-request top-31 selection + new K/V write, then layout,
+req_to_token gather and attention.  The step is captured once in a HIP graph
+and replayed; seq_lens advance by one token per replay, so pages complete and
+get finalized during the run.  Reported value: microseconds per layer-step
+(step time / 48).  The roofline's `traffic` is read from the committed
+rocprofv3 PMC summary in profiles/ (copy-calibrated FETCH_SIZE + WRITE_SIZE).
 
     python bench.py [--steps K] [--warmup W]
 """
@@ -31,6 +33,19 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+PROFILE = os.path.join(ROOT, "profiles", "quest_layer_step_kernels_b16_128k.md")
+
+
+def profiled_traffic() -> dict:
+    """HBM bytes per launch of each layer-step kernel, from the committed rocprofv3 PMC
+    summary (FETCH_SIZE + WRITE_SIZE, copy-calibrated); {} when the summary is absent."""
+    try:
+        for line in open(PROFILE):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return {k: int(v) for k, v in (kv.split("=") for kv in line.split(":", 1)[1].split())}
+    except OSError:
+        pass
+    return {}
 
 
 class Layer:
@@ -97,7 +112,19 @@ def main() -> int:
     ap.add_argument("--layers", type=int, default=48)
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--cpu-sample", type=int, default=2, help="requests in the CPU-baseline sample (0 = skip)")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a plain device copy of MIB MiB three times (scale for the HBM byte counters)")
     args = ap.parse_args()
+    if args.copy_calibration:
+        n = args.copy_calibration << 20
+        src = torch.empty(n, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        src.fill_(1)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": n, "copies": 3}))
+        return 0
     if args.gpus != 1:
         print("bench.py measures one GPU: the path shards by request with no cross-GPU traffic, "
               "and this build runs on a single MI355X; use --gpus 1", file=sys.stderr)
@@ -190,7 +217,7 @@ def main() -> int:
     ms_att = time_graph(attend, L, stream)
     bw_sel = byts["bounds"] / (ms_sel * 1e-3) / 1e9
     bw_att = byts["kv"] / (ms_att * 1e-3) / 1e9
-    dominant = ("quest_attend_head_kernel", ms_att, byts["kv"], bw_att) if ms_att >= ms_sel else (
+    dominant = ("quest_attend_part_kernel", ms_att, byts["kv"], bw_att) if ms_att >= ms_sel else (
         "quest_score_select_kernel", ms_sel, byts["bounds"], bw_sel)
 
     cpu = None
@@ -222,10 +249,10 @@ def main() -> int:
         "tokens_per_s": round(B / (ms_per_step * 1e-3), 1),
         "algorithmic_bytes_per_layer_step": byts,
         "kernels_us": {"quest_score_select_kernel": round(ms_sel * 1e3, 2),
-                       "quest_attend_head_kernel": round(ms_att * 1e3, 2)},
+                       "quest_attend_part_kernel": round(ms_att * 1e3, 2)},
         "roofline": {"kernel": dominant[0], "bound": "hbm", "achieved": round(dominant[3], 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(dominant[3] / HBM_PEAK_GBS, 4),
-                     "traffic": None},
+                     "traffic": profiled_traffic().get(dominant[0])},
         "cpu_baseline": cpu,
         "setup_s": round(setup_s, 1),
     }
