@@ -203,15 +203,21 @@ def main() -> int:
     step_frac = byts["headline"] / (us_per_layer_step * 1e-6) / (HBM_PEAK_GBS * 1e9)
 
     # per-kernel durations of the layer step's two launches (score + select, attention),
-    # each from a graph of L launches at the same shapes, HIP events on the launch stream
+    # each from a graph of L launches over the L layers in turn (so that no launch finds its
+    # bounds or K/V rows in a cache, as in the step), HIP events on the launch stream
     torch.add(base, seq_lens - 1, out=out_loc)
     be.quest.prepare_step(seq_lens)
+    turn = {"sel": 0, "att": 0}
 
     def score_select():
-        be.forward_decode_phase(q_all[0], k_new[0], v_new[0], layers[0], batch, 1)
+        i = turn["sel"] % L
+        turn["sel"] += 1
+        be.forward_decode_phase(q_all[i], k_new[i], v_new[i], layers[i], batch, 1)
 
     def attend():
-        be.forward_decode_phase(q_all[0], k_new[0], v_new[0], layers[0], batch, 2)
+        i = turn["att"] % L
+        turn["att"] += 1
+        be.forward_decode_phase(q_all[i], k_new[i], v_new[i], layers[i], batch, 2)
 
     ms_sel = time_graph(score_select, L, stream)
     ms_att = time_graph(attend, L, stream)

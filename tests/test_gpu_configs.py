@@ -1,0 +1,269 @@
+"""Parity at the path's own full-size configurations (Qwen3-30B-A3B shapes: 32 q / 4 KV
+heads x 128, bf16, page 64, top_k 2048 = 31 selected pages + the recent 64):
+
+* batch 8 x 32768 tokens, keys N(0,1) plus a per-(request, page) mean offset N(0, 0.5);
+* a 48-layer ragged sweep, batch 16, contexts uniform in [8192, 131072], 64 decode steps
+  (every step appends one token per request; pages complete and are finalized);
+* batch 4 x 262144 tokens, 4 outlier channels per KV head scaled x10, 256 decode steps,
+  both overlap modes, quest and quest_hisparse.
+
+Inputs are generated on the device from fixed seeds and copied to the host for the
+oracle; positions are compared bit for bit, attention within 2e-2 (bf16).  Where the
+oracle would need the whole batch in host memory (the 48-layer sweep) it follows sampled
+(layer, request) pairs from their own K rows.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as oa
+from oracle import bf16
+from oracle import quest as oq
+from tests.conftest import bf16_bits
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda", 0)
+H, KV, D, P, TOP_K = 32, 4, 128, 64, 2048
+SCALE = D**-0.5
+
+
+class Layer:
+    def __init__(self, i):
+        self.layer_id, self.scaling = i, SCALE
+
+
+def dev_randn(shape, seed):
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    return torch.randn(shape, generator=g, device=DEV, dtype=torch.float32)
+
+
+def oracle_attention(q_row, k_rows, v_rows):
+    """q_row [H, D] bf16, k_rows / v_rows [n, KV, D] bf16 (CPU) -> [H*D] float32."""
+    kb = bf16.to_f32(bf16_bits(k_rows))
+    vb = bf16.to_f32(bf16_bits(v_rows))
+    return oa.decode_attention(q_row.float().numpy(), kb, vb, SCALE).reshape(-1)
+
+
+def make_quest_backend(B, ctx, L, avoid=False, hisparse=False):
+    from qwenquest_amd.attention.quest_hisparse import QuestHiSparseBackend
+    from qwenquest_amd.attention.quest_only import QuestOnlyBackend
+    from qwenquest_amd.memory import MHATokenToKVPool, ReqToTokenPool
+
+    rtp = ReqToTokenPool(B, ctx, DEV)
+    kvp = MHATokenToKVPool(B * ctx, L, KV, D, torch.bfloat16, DEV)
+    cfg = {"algorithm": "quest", "top_k": TOP_K, "quest_page_size": P, "avoid_recent_overlap": avoid}
+    if hisparse:
+        be = QuestHiSparseBackend(rtp, kvp, cfg, host_pool_size=B * ctx)
+    else:
+        be = QuestOnlyBackend(rtp, kvp, cfg)
+    base = 1 + torch.arange(B, device=DEV, dtype=torch.int64) * ctx
+    rtp.req_to_token.copy_((base[:, None] + torch.arange(ctx, device=DEV)[None]).to(torch.int32))
+    return rtp, kvp, be, base
+
+
+def test_batch8_32k_per_page_offsets():
+    """Batch 8 x 32768 tokens, one layer, 4 decode steps through QuestOnlyBackend (fused
+    two-launch step): positions bit-exact vs the oracle, attention within 2e-2."""
+    from qwenquest_amd.batch import ForwardBatch, ForwardMode
+
+    B, S, steps = 8, 32768, 4
+    ctx = S + steps + 64
+    rtp, kvp, be, base = make_quest_backend(B, ctx, 1)
+    # k = N(0,1) + mu[request, page], mu ~ N(0, 0.5); row 1 + r*ctx + p holds position p
+    mu = dev_randn((B, (ctx + P - 1) // P), 11) * 0.5
+    rows_pos = torch.arange(ctx, device=DEV)
+    k = dev_randn((B, ctx, KV, D), 12) + mu[:, rows_pos // P][:, :, None, None]
+    kvp.k_all[0, 1:].copy_(k.reshape(B * ctx, KV, D).to(torch.bfloat16))
+    kvp.v_all[0, 1:].copy_(dev_randn((B * ctx, KV, D), 13).to(torch.bfloat16))
+    del k
+    prompt = S - 1
+    for r in range(B):
+        be.quest.update_prefill_representations_fused(r, kvp.k_all, rtp.req_to_token[r, :prompt])
+        be._skip_first_decode_update[r] = True
+    kk, vv = kvp.k_all[0].cpu(), kvp.v_all[0].cpu()
+    kbits = bf16_bits(kk)
+    st = oq.QuestState(TOP_K, P)
+    st.init_storage(0, 1, B, ctx, KV, D)
+    for r in range(B):
+        st.update_prefill_representations(0, r, kbits, (1 + r * ctx + np.arange(prompt)))
+    reqs = list(range(B))
+    for step in range(steps):
+        seq = torch.full((B,), S + step, device=DEV, dtype=torch.int64)
+        loc = base + seq - 1
+        batch = ForwardBatch(ForwardMode.DECODE, None, None, torch.arange(B, device=DEV), seq, loc, rtp, kvp, be)
+        be.init_forward_metadata(batch)
+        if step > 0:
+            st.update_decode_representations(0, reqs, kbits, (loc - 1).cpu().numpy())
+            st.maybe_finalize_decode_representations(reqs)
+        st.prepare_step(seq.cpu().numpy())
+        q = dev_randn((B, H, D), 100 + step).to(torch.bfloat16)
+        lc = loc.cpu()
+        out = be.forward_decode(q, kk[lc].to(DEV), vv[lc].to(DEV), Layer(0), batch).float().cpu().numpy()
+        pos = be._positions[:B].cpu().numpy()
+        ref_pos, ref_actual, _ = st.retrieve_topk(q.float().cpu().numpy(), 0, reqs)
+        qc = q.cpu()
+        for i in range(B):
+            n = int(ref_actual[i])
+            assert n == TOP_K
+            assert np.array_equal(pos[i, :n], ref_pos[i, :n]), f"step {step} request {i}"
+            rows = torch.from_numpy(1 + i * ctx + ref_pos[i, :n].astype(np.int64))
+            ref = oracle_attention(qc[i], kk[rows], vv[rows])
+            assert np.abs(out[i] - ref).max() < 2e-2, f"step {step} request {i}"
+
+
+def test_ragged_48_layer_sweep_sampled():
+    """48 layers, batch 16, contexts uniform in [8192, 131072] (seeded), 64 decode steps with
+    one append per request per step, all layers through QuestOnlyBackend.  Sampled
+    (layer, request) pairs follow the oracle from their own K rows: positions bit-exact at
+    sampled steps, attention within 2e-2, and the pair's page bounds / running bounds
+    bit-exact after the last step (pages completed during the sweep included)."""
+    from qwenquest_amd.attention.quest_only import QuestOnlyBackend
+    from qwenquest_amd.batch import ForwardBatch, ForwardMode
+    from qwenquest_amd.memory import MHATokenToKVPool, ReqToTokenPool
+
+    L, B, steps = 48, 16, 64
+    gen = np.random.default_rng(2024)
+    ctxs = gen.integers(8192, 131072, size=B, endpoint=True)
+    ctx = int(ctxs.max()) + steps + 64
+    # request r's rows are packed after r-1's: its context plus room for the decode steps
+    span = ctxs + steps + 64
+    starts = 1 + np.concatenate([[0], np.cumsum(span)[:-1]])
+    pool = int(span.sum())
+    rtp = ReqToTokenPool(B, ctx, DEV)
+    kvp = MHATokenToKVPool(pool, L, KV, D, torch.bfloat16, DEV)
+    be = QuestOnlyBackend(rtp, kvp, {"algorithm": "quest", "top_k": TOP_K, "quest_page_size": P})
+    base = torch.tensor(starts, device=DEV, dtype=torch.int64)
+    rtp.req_to_token.copy_((base[:, None] + torch.arange(ctx, device=DEV)[None]).clamp(max=pool).to(torch.int32))
+    for layer in range(L):
+        kvp.k_all[layer].copy_(dev_randn((pool + 1, KV, D), 1000 + layer).to(torch.bfloat16))
+        kvp.v_all[layer].copy_(dev_randn((pool + 1, KV, D), 2000 + layer).to(torch.bfloat16))
+    prompts = [int(c) - 1 for c in ctxs]  # the first decode step has seq_len = ctxs[r]
+    for r in range(B):
+        be.quest.update_prefill_representations_fused(r, kvp.k_all, rtp.req_to_token[r, : prompts[r]])
+        be._skip_first_decode_update[r] = True
+    samples = [(0, int(np.argmax(ctxs))), (23, int(np.argmin(ctxs))), (47, 5)]
+    oracles = {}
+    for layer, r in samples:
+        st = oq.QuestState(TOP_K, P)
+        st.init_storage(layer, layer + 1, 1, ctx, KV, D)
+        rows = int(starts[r]) + torch.arange(prompts[r], device=DEV)
+        st.update_prefill_representations(layer, 0, bf16_bits(kvp.k_all[layer, rows]), np.arange(prompts[r]))
+        oracles[(layer, r)] = st
+    check_steps = {0, 1, 31, 62, 63}
+    seq = torch.tensor(ctxs, device=DEV, dtype=torch.int64)
+    loc = torch.empty(B, device=DEV, dtype=torch.int64)
+    batch = ForwardBatch(ForwardMode.DECODE, None, None, torch.arange(B, device=DEV), seq, loc, rtp, kvp, be)
+    for step in range(steps):
+        torch.add(base, seq - 1, out=loc)
+        be.init_forward_metadata(batch)
+        kn = dev_randn((L, B, KV, D), 3000 + step).to(torch.bfloat16)
+        vn = dev_randn((L, B, KV, D), 4000 + step).to(torch.bfloat16)
+        q = dev_randn((L, B, H, D), 5000 + step).to(torch.bfloat16)
+        seqs = seq.cpu().numpy()
+        for (layer, r), st in oracles.items():
+            if step > 0:  # fold the previous decode token (its K arrived through forward_decode)
+                prev = bf16_bits(kvp.k_all[layer, int(base[r]) + int(seqs[r]) - 2][None])
+                st.update_decode_representations(layer, [0], prev, [0])
+                st.maybe_finalize_decode_representations([0])
+            st.prepare_step(seqs[r : r + 1])
+        for layer in range(L):
+            out = be.forward_decode(q[layer], kn[layer], vn[layer], Layer(layer), batch)
+            for (sl, r), st in oracles.items():
+                if sl != layer or step not in check_steps:
+                    continue
+                pos = be._positions[r].cpu().numpy()
+                ref_pos, ref_actual, _ = st.retrieve_topk(q[layer, r : r + 1].float().cpu().numpy(), layer, [0])
+                n = int(ref_actual[0])
+                assert np.array_equal(pos[:n], ref_pos[0, :n]), f"step {step} layer {layer} request {r}"
+                rows = (int(base[r]) + torch.from_numpy(ref_pos[0, :n].astype(np.int64))).to(DEV)
+                ref = oracle_attention(q[layer, r].cpu(), kvp.k_all[layer, rows].cpu(), kvp.v_all[layer, rows].cpu())
+                assert np.abs(out[r].float().cpu().numpy() - ref).max() < 2e-2, f"step {step} layer {layer}"
+        seq.add_(1)
+    torch.cuda.synchronize()
+    for (layer, r), st in oracles.items():
+        assert np.array_equal(bf16_bits(be.quest.page_k_bounds[layer, r]), st.page_k_bounds[0, 0])
+        assert np.array_equal(bf16_bits(be.quest.running_k_min[layer, r]), st.running_k_min[0, 0])
+        assert np.array_equal(bf16_bits(be.quest.running_k_max[layer, r]), st.running_k_max[0, 0])
+        assert int(be.quest.running_page_idx[r]) == int(st.running_page_idx[0])
+        assert int(be.quest.running_token_count[r]) == int(st.running_token_count[0])
+    del rtp, kvp, be
+    torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("avoid", [False, True])
+def test_batch4_262k_outliers_quest_and_hisparse(avoid):
+    """Batch 4 x 262144 tokens (4096+ pages), keys N(0,1) with 4 seeded outlier channels per
+    KV head x10, 256 decode steps in one overlap mode: QuestOnlyBackend and
+    QuestHiSparseBackend give bit-identical positions and outputs at every step; positions
+    bit-exact vs the oracle on sampled steps, attention within 2e-2."""
+    from qwenquest_amd.batch import ForwardBatch, ForwardMode
+
+    B, S, steps = 4, 262144, 256
+    ctx = S + steps + 64
+    gen = torch.Generator().manual_seed(77)
+    outl = torch.stack([torch.randperm(D, generator=gen)[:4] for _ in range(KV)])  # [KV, 4]
+    scale = torch.ones(KV, D)
+    scale[torch.arange(KV)[:, None], outl] = 10.0
+    k = (dev_randn((B * ctx + 1, KV, D), 21) * scale.to(DEV)).to(torch.bfloat16)
+    v = dev_randn((B * ctx + 1, KV, D), 22).to(torch.bfloat16)
+    qs = dev_randn((steps, B, H, D), 23).to(torch.bfloat16)
+    prompt = S - 1
+    kk, vv = k.cpu(), v.cpu()
+    kbits = bf16_bits(kk)
+    st = oq.QuestState(TOP_K, P, avoid_recent_overlap=avoid)
+    st.init_storage(0, 1, B, ctx, KV, D)
+    for r in range(B):
+        st.update_prefill_representations(0, r, kbits, 1 + r * ctx + np.arange(prompt))
+    check_steps = set(range(0, steps, 16)) | {steps - 1}
+    attn_steps = {0, 64, 255}
+    reqs = list(range(B))
+    results = {}
+    for mode in ("quest", "quest_hisparse"):
+        rtp, kvp, be, base = make_quest_backend(B, ctx, 1, avoid=avoid, hisparse=mode == "quest_hisparse")
+        kvp.k_all[0].copy_(k)
+        kvp.v_all[0].copy_(v)
+        pre = ForwardBatch(ForwardMode.EXTEND, None, None, torch.arange(B), torch.full((B,), prompt), None,
+                           rtp, kvp, be)
+        if mode == "quest":
+            be._update_quest_for_extend(pre)
+        else:
+            be.on_extend_finished(pre)
+        outs, poss = [], []
+        for step in range(steps):
+            seq = torch.full((B,), S + step, device=DEV, dtype=torch.int64)
+            loc = base + seq - 1
+            batch = ForwardBatch(ForwardMode.DECODE, None, None, torch.arange(B, device=DEV), seq,
+                                 loc if mode == "quest" else None, rtp, kvp, be)
+            be.init_forward_metadata(batch)
+            out = be.forward_decode(qs[step], k[loc], v[loc], Layer(0), batch)
+            outs.append(out.cpu())
+            poss.append(be._positions[:B].cpu())
+        results[mode] = (torch.stack(outs), torch.stack(poss))
+        if mode == "quest_hisparse":
+            s = be.coord.stats
+            assert s.misses > 0 and s.hits > 0
+        del rtp, kvp, be
+        torch.cuda.empty_cache()
+    assert torch.equal(results["quest"][1], results["quest_hisparse"][1])
+    assert torch.equal(results["quest"][0], results["quest_hisparse"][0])
+    outs, poss = results["quest"]
+    for step in range(steps):
+        seqs = np.full(B, S + step)
+        if step > 0:
+            st.update_decode_representations(0, reqs, kbits, 1 + np.arange(B) * ctx + seqs - 2)
+            st.maybe_finalize_decode_representations(reqs)
+        st.prepare_step(seqs)
+        if step not in check_steps:
+            continue
+        ref_pos, ref_actual, _ = st.retrieve_topk(qs[step].float().cpu().numpy(), 0, reqs)
+        for i in range(B):
+            n = int(ref_actual[i])
+            assert np.array_equal(poss[step, i, :n].numpy(), ref_pos[i, :n]), f"step {step} request {i}"
+            if step in attn_steps:
+                rows = torch.from_numpy(1 + i * ctx + ref_pos[i, :n].astype(np.int64))
+                ref = oracle_attention(qs[step, i].cpu(), kk[rows], vv[rows])
+                assert np.abs(outs[step, i].float().numpy() - ref).max() < 2e-2, f"step {step} request {i}"
