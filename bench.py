@@ -16,6 +16,14 @@ get finalized during the run.  Reported value: microseconds per layer-step
 rocprofv3 PMC summary in profiles/ (copy-calibrated FETCH_SIZE + WRITE_SIZE).
 
     python bench.py [--steps K] [--warmup W]
+
+`--hisparse` measures the quest_hisparse tier instead (batch 16, 128K context,
+a hot buffer of 4096 + 1 rows per request and layer, the full K/V history in
+pinned host memory, queries AR(1) with rho 0.9 across steps): swap-in rows per
+layer-step, the swap-in's H2D rate next to the pinned hipMemcpy H2D peak
+measured in the same run, and the decode time per layer-step.  Its pinned host
+tier holds `--hisparse-layers` layers (default 4; the per-layer work is the
+same for all 48).
 """
 
 from __future__ import annotations
@@ -102,6 +110,116 @@ def cpu_baseline(top_k, page, heads, kv, dim, ctx, sample_reqs: int) -> dict:
     return {"per_request_s": float(np.median(times)), "reqs": sample_reqs}
 
 
+def pinned_h2d_peak(nbytes: int = 1 << 30, reps: int = 5) -> float:
+    """GB/s of hipMemcpy (torch copy) from pinned host memory into device memory."""
+    src = torch.empty(nbytes, dtype=torch.uint8, pin_memory=True)
+    dst = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    dst.copy_(src, non_blocking=True)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        dst.copy_(src, non_blocking=True)
+    e1.record()
+    e1.synchronize()
+    return nbytes * reps / (e0.elapsed_time(e1) * 1e-3) / 1e9
+
+
+def hisparse_bench(args) -> int:
+    """quest_hisparse decode (QuestHiSparseBackend, the drop-in path), swap-in measured with
+    HIP events around each swap-in call on the launch stream."""
+    from qwenquest_amd.attention.quest_hisparse import QuestHiSparseBackend
+    from qwenquest_amd.batch import ForwardBatch, ForwardMode
+    from qwenquest_amd.memory import MHATokenToKVPool, ReqToTokenPool
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    B, S, L = args.batch, args.ctx, args.hisparse_layers
+    H, KV, D, P, TOP_K, BUF = 32, 4, 128, 64, 2048, 4096
+    steps = args.warmup + args.steps
+    max_ctx = S + steps + 64
+    t_setup = time.perf_counter()
+    rtp = ReqToTokenPool(B, max_ctx, dev)
+    kvp = MHATokenToKVPool(B * max_ctx, L, KV, D, torch.bfloat16, dev)
+    gen = torch.Generator(device=dev).manual_seed(4321)
+    for layer in range(L):
+        kvp.k_all[layer].normal_(generator=gen)
+        kvp.v_all[layer].normal_(generator=gen)
+    base = 1 + torch.arange(B, device=dev, dtype=torch.int64) * max_ctx
+    rtp.req_to_token.copy_((base[:, None] + torch.arange(max_ctx, device=dev)[None]).to(torch.int32))
+    be = QuestHiSparseBackend(rtp, kvp, {"algorithm": "quest", "top_k": TOP_K, "quest_page_size": P,
+                                         "device_buffer_size": BUF}, host_pool_size=B * max_ctx)
+    prompt = S - 1
+    pre = ForwardBatch(ForwardMode.EXTEND, None, None, torch.arange(B), torch.full((B,), prompt), None, rtp, kvp, be)
+    be.on_extend_finished(pre)
+    torch.cuda.synchronize()
+    setup_s = time.perf_counter() - t_setup
+
+    coord = be.coord
+    swap = coord.swap_in_selected_pages
+    events = []
+
+    def timed_swap(*a, **kw):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        rows = swap(*a, **kw)
+        e1.record()
+        events.append((e0, e1))
+        return rows
+
+    coord.swap_in_selected_pages = timed_swap
+    layers = [Layer(i, D**-0.5) for i in range(L)]
+    rho = 0.9
+    q = torch.randn((L, B, H, D), generator=gen, device=dev)
+    seq = torch.full((B,), S, device=dev, dtype=torch.int64)
+    rpi = torch.arange(B, device=dev, dtype=torch.int64)
+    step_ms, swap_ms, misses = [], [], []
+    for step in range(steps):
+        q = rho * q + (1 - rho**2) ** 0.5 * torch.randn((L, B, H, D), generator=gen, device=dev)
+        qb = q.to(torch.bfloat16)
+        kn = torch.randn((L, B, KV, D), generator=gen, device=dev).to(torch.bfloat16)
+        vn = torch.randn((L, B, KV, D), generator=gen, device=dev).to(torch.bfloat16)
+        m0 = coord.stats.misses
+        events.clear()
+        batch = ForwardBatch(ForwardMode.DECODE, None, None, rpi, seq, None, rtp, kvp, be)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        be.init_forward_metadata(batch)
+        for layer in range(L):
+            be.forward_decode(qb[layer], kn[layer], vn[layer], layers[layer], batch)
+        e1.record()
+        e1.synchronize()
+        if step >= args.warmup:
+            step_ms.append(e0.elapsed_time(e1))
+            swap_ms.append(sum(a.elapsed_time(b) for a, b in events))
+            misses.append(coord.stats.misses - m0)
+        seq.add_(1)
+    row_bytes = 2 * KV * D * 2  # K + V row
+    miss_rows = float(np.mean(misses)) / L
+    swap_us = float(np.mean(swap_ms)) * 1e3 / L
+    h2d = miss_rows * row_bytes / (swap_us * 1e-6) / 1e9 if swap_us > 0 else 0.0
+    peak = pinned_h2d_peak()
+    st = coord.stats
+    print(json.dumps({
+        "metric": "quest_hisparse decode @128K ctx, batch 16: swap-in H2D GB/s and us per layer-step",
+        "value": round(h2d, 2), "unit": "GB/s (swap-in misses x 2 KiB / swap-in time)",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
+        "dtype": "bf16", "data": "synthetic N(0,1) K/V, AR(1) queries rho 0.9, fixed seeds",
+        "config": {"workload": f"quest_hisparse decode, batch {B}, {S}-token context, hot buffer {BUF}+1 rows, "
+                               f"{L} layers resident in pinned host memory", "batch": B, "seq_len": S, "layers": L},
+        "us_per_layer_step": round(float(np.mean(step_ms)) * 1e3 / L, 2),
+        "swap_in_us_per_layer_step": round(swap_us, 2),
+        "swap_in_rows_per_layer_step": round(miss_rows, 1),
+        "hit_rate": round(st.hit_rate, 4),
+        "h2d_pinned_memcpy_peak_gbs": round(peak, 2),
+        "h2d_frac_of_memcpy_peak": round(h2d / peak, 4) if peak > 0 else None,
+        "h2d_frac_of_64gbs_nominal": round(h2d / 64.0, 4),
+        "setup_s": round(setup_s, 1),
+    }))
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -114,6 +232,8 @@ def main() -> int:
     ap.add_argument("--cpu-sample", type=int, default=2, help="requests in the CPU-baseline sample (0 = skip)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB three times (scale for the HBM byte counters)")
+    ap.add_argument("--hisparse", action="store_true", help="measure the quest_hisparse tier instead")
+    ap.add_argument("--hisparse-layers", type=int, default=4)
     args = ap.parse_args()
     if args.copy_calibration:
         n = args.copy_calibration << 20
@@ -129,6 +249,8 @@ def main() -> int:
         print("bench.py measures one GPU: the path shards by request with no cross-GPU traffic, "
               "and this build runs on a single MI355X; use --gpus 1", file=sys.stderr)
         return 2
+    if args.hisparse:
+        return hisparse_bench(args)
 
     from qwenquest_amd import _lib
     from qwenquest_amd.attention.quest_only import QuestOnlyBackend
