@@ -157,12 +157,28 @@ int qq_quest_decode_attention(const void* q, int q_dtype, int64_t q_batch_stride
 /* Replaces the Mode-3 attention of QuestHiSparseBackend.forward_decode
  * (src/qwenquest/attention/quest_hisparse.py:294-300): like
  * qq_quest_decode_attention but rows come directly from `rows` [bs, rows_stride]
- * int64 (the hot-buffer rows returned by the swap-in). */
+ * int64 (the hot-buffer rows returned by the swap-in).  With `sync` (>=
+ * qq_quest_layer_step_sync_bytes(bs, kv_heads), zeroed before the first call),
+ * bf16, KV*D = 4*128, G <= 16 and rows_stride <= 4096 slots, it runs the
+ * attention kernel of qq_quest_forward_decode's fused path over the given rows
+ * (same arithmetic in the same slot order: pass `sync` exactly when
+ * qq_quest_fused_step holds for the quest configuration, and quest_hisparse
+ * matches quest bit for bit); otherwise chunked MFMA attention + merge, as
+ * qq_quest_decode_attention. */
 int qq_decode_attention_rows(const void* q, int q_dtype, int64_t q_batch_stride, int num_q_heads,
                              const void* k_layer, const void* v_layer, int kv_dtype,
                              int64_t kv_rows, int kv_heads, int head_dim, const int64_t* rows,
                              int64_t rows_stride, const int32_t* actual_lens, int bs, float scale,
-                             void* out, void* workspace, int64_t workspace_bytes, void* stream);
+                             void* out, void* workspace, int64_t workspace_bytes, void* sync,
+                             int64_t sync_bytes, void* stream);
+
+/* 1 when qq_quest_forward_decode with a sync buffer runs the fused layer step
+ * for these shapes (bf16, KV*D = 4*128, G <= 16, page 64, at most 64 selected
+ * pages, top_k <= 4096, max_pages <= 6144; new_dtype -1 = no new token), else
+ * 0.  No counterpart in the reference: it lets a caller of
+ * qq_decode_attention_rows choose the same attention arithmetic. */
+int qq_quest_fused_step(int q_dtype, int kv_dtype, int new_dtype, int num_q_heads, int kv_heads,
+                        int head_dim, int page_size, int top_k, int max_pages);
 
 /* Bytes of the sync buffer qq_quest_forward_decode's two-launch path uses for
  * `bs` requests (one counter per request and per (request, KV head), each on
@@ -180,8 +196,8 @@ int64_t qq_quest_layer_step_sync_bytes(int bs, int kv_heads);
  * prepare_step outputs; workspace sized by
  * qq_decode_attention_workspace_bytes(bs, top_k, H, D).
  * With `sync` (>= qq_quest_layer_step_sync_bytes, zeroed before the first
- * call), bf16 tensors, KV*D = 4*128, page 64, top_k/P - 1 <= 64 and
- * max_pages <= 4096, the layer runs as two launches (score + select, then
+ * call) and the shapes of qq_quest_fused_step (bf16 tensors, KV*D = 4*128,
+ * page 64, top_k/P - 1 <= 64, max_pages <= 6144), the layer runs as two launches (score + select, then
  * attention + merge; the selection and the merge hand off inside them);
  * otherwise, or with sync == NULL, as four launches.  Calls sharing one sync
  * buffer must not overlap (one stream). */

@@ -52,8 +52,9 @@ SIGNATURES: dict[str, tuple] = {
     ),
     "qq_decode_attention_rows": (
         _I,
-        [_P, _I, _L, _I, _P, _P, _I, _L, _I, _I, _P, _L, _P, _I, _F, _P, _P, _L, _P],
+        [_P, _I, _L, _I, _P, _P, _I, _L, _I, _I, _P, _L, _P, _I, _F, _P, _P, _L, _P, _L, _P],
     ),
+    "qq_quest_fused_step": (_I, [_I, _I, _I, _I, _I, _I, _I, _I, _I]),
     "qq_quest_forward_decode": (
         _I,
         [_P, _I, _L, _I, _P, _P, _I, _P, _P, _P, _I, _L, _P, _I, _P, _P, _P, _P, _I, _I, _I, _I,

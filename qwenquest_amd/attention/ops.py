@@ -49,11 +49,15 @@ def decode_attention_rows(
     *,
     workspace: AttentionWorkspace | None = None,
     out: torch.Tensor | None = None,
+    sync: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Batched form: request ``i`` attends ``q[i] [H, D]`` over ``k_buf[rows[i, :actual_lens[i]]]``.
 
     ``rows`` ``[bs, >= max(actual_lens)]`` int64, ``k_buf``/``v_buf`` ``[rows, KV, D]``.
-    Returns ``[bs, H*D]`` in q's dtype.
+    Returns ``[bs, H*D]`` in q's dtype.  With ``sync`` (a zeroed uint8 buffer of at least
+    ``qq_quest_layer_step_sync_bytes`` bytes) the bf16 KV*D = 4*128 shapes run the attention
+    kernel of the fused Quest layer step, whose arithmetic QuestHiSparseBackend shares with
+    QuestOnlyBackend.
     """
     bs, heads, dim = q.shape
     kv = k_buf.shape[1]
@@ -67,7 +71,8 @@ def decode_attention_rows(
         "qq_decode_attention_rows", _lib.ptr(q), _lib.dtype_code(q.dtype), q.stride(0), heads,
         _lib.ptr(k_buf), _lib.ptr(v_buf), _lib.dtype_code(k_buf.dtype), k_buf.shape[0], kv, dim,
         _lib.ptr(rows), rows.stride(0), _lib.ptr(actual), bs, float(scaling), _lib.ptr(res),
-        _lib.ptr(buf), buf.numel(), _lib.stream(q.device),
+        _lib.ptr(buf), buf.numel(), _lib.ptr(sync) if sync is not None else None,
+        sync.numel() if sync is not None else 0, _lib.stream(q.device),
     )
     return res
 

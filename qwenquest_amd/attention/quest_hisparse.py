@@ -17,6 +17,7 @@ from typing import TYPE_CHECKING, Any
 
 import torch
 
+from qwenquest_amd import _lib
 from qwenquest_amd.attention.base import AttentionBackend
 from qwenquest_amd.attention.ops import AttentionWorkspace, decode_attention_rows
 from qwenquest_amd.config import SparseConfig, parse_hisparse_config
@@ -81,6 +82,12 @@ class QuestHiSparseBackend(AttentionBackend):
         )
         self._positions = torch.empty((req_to_token_pool.size, cfg.top_k), dtype=torch.int32, device=device)
         self._attn_ws = AttentionWorkspace(device)
+        # QuestOnlyBackend runs its fused layer step for some shapes; the attention over the
+        # hot-buffer rows then runs the same kernel (counters in this zeroed buffer), so the
+        # two modes give the same bits
+        sync_bytes = int(_lib.load().qq_quest_layer_step_sync_bytes(req_to_token_pool.size, token_to_kv_pool.kv_heads))
+        self._attn_sync = torch.zeros(max(sync_bytes, 4), dtype=torch.uint8, device=device)
+        self._fused_cache: dict[tuple, bool] = {}
 
     def init_forward_metadata(self, batch: ForwardBatch) -> None:
         if batch.forward_mode.is_decode():
@@ -93,6 +100,19 @@ class QuestHiSparseBackend(AttentionBackend):
             prefill_indices = self.req_to_token[req_idx, :seq_len]
             self.coord.admit_request(req_idx, seq_len, self.token_to_kv_pool, prefill_indices)
 
+    def _fused_attention(self, q3: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> bool:
+        """Whether QuestOnlyBackend.forward_decode would run the fused layer step for these
+        tensors (its new K/V dtype rule: k's dtype if k and v share bf16 or fp32, else the pool's)."""
+        pool_dtype = self.token_to_kv_pool.dtype
+        new_dtype = k.dtype if k.dtype == v.dtype and k.dtype in (torch.bfloat16, torch.float32) else pool_dtype
+        key = (q3.dtype, new_dtype, q3.shape[1])
+        if key not in self._fused_cache:
+            qa, pool = self.quest, self.token_to_kv_pool
+            self._fused_cache[key] = bool(_lib.load().qq_quest_fused_step(
+                _lib.dtype_code(q3.dtype), _lib.dtype_code(pool_dtype), _lib.dtype_code(new_dtype), q3.shape[1],
+                pool.kv_heads, pool.head_dim, qa.page_size, qa.top_k, qa.max_pages_per_req))
+        return self._fused_cache[key]
+
     def forward_decode(self, q, k, v, layer, batch: ForwardBatch) -> torch.Tensor:
         """quest_hisparse.py:112-133."""
         reqs, seq_lens = batch.req_pool_indices, batch.seq_lens
@@ -104,6 +124,7 @@ class QuestHiSparseBackend(AttentionBackend):
         return decode_attention_rows(
             q3, self.coord.device_k[layer.layer_id], self.coord.device_v[layer.layer_id], rows, actual,
             layer.scaling, workspace=self._attn_ws,
+            sync=self._attn_sync if self._fused_attention(q3, k, v) else None,
         ).view(bs, -1)
 
     def on_request_finished(self, req_pool_idx: int) -> None:

@@ -360,7 +360,8 @@ extern "C" int qq_decode_attention_rows(const void* q, int q_dtype, int64_t q_ba
                                         int kv_dtype, int64_t kv_rows, int kv_heads, int head_dim,
                                         const int64_t* rows, int64_t rows_stride,
                                         const int32_t* actual_lens, int bs, float scale, void* out,
-                                        void* workspace, int64_t workspace_bytes, void* stream) {
+                                        void* workspace, int64_t workspace_bytes, void* sync,
+                                        int64_t sync_bytes, void* stream) {
   const char* what = "qq_decode_attention_rows";
   if (bs == 0) return QQ_OK;
   AttnArgs a;
@@ -368,6 +369,11 @@ extern "C" int qq_decode_attention_rows(const void* q, int q_dtype, int64_t q_ba
                        kv_rows, kv_heads, head_dim, actual_lens, scale, out, what);
   if (st != QQ_OK) return st;
   QQ_REQUIRE(rows && rows_stride > 0, "%s: null row list", what);
+  if (sync && q_dtype == QQ_DTYPE_BF16 && kv_dtype == QQ_DTYPE_BF16 && kv_heads == 4 && head_dim == kMfmaDim &&
+      attend_rows_fused(q, q_batch_stride, num_q_heads, k_layer, v_layer, kv_rows, rows, rows_stride, actual_lens, bs,
+                        scale, out, workspace, workspace_bytes, sync, sync_bytes,
+                        static_cast<hipStream_t>(stream)) == QQ_OK)
+    return check_launch(what);
   a.rows = rows;
   a.pos_stride = rows_stride;
   return launch_attention(a, kv_dtype, bs, workspace_bytes, workspace, static_cast<hipStream_t>(stream), what);

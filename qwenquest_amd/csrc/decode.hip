@@ -3,7 +3,7 @@
 // token's K/V, select the positions, gather through req_to_token and attend.
 //
 // Fused path (bf16, KV*D = 4*128, page 64, at most 64 selected pages, at most
-// 4096 pages per request, top_k <= 4096, and a zeroed sync buffer from the
+// 6144 pages per request, top_k <= 4096, and a zeroed sync buffer from the
 // caller): two launches.
 //   1. score + select, one block per (request, 32 candidate pages), the whole
 //      grid resident at once: 4 waves x 8 pages scored, scores out with
@@ -57,6 +57,9 @@ struct StepArgs {
   uint32_t* sync;
   int bs, tiles_s, G;
   int parts, per_wave;     // attention blocks per (request, KV head); rows per wave
+  const int64_t* rows_in;  // rows given [bs, rows_stride] (attention over given rows)
+  int64_t rows_stride;
+  const int32_t* actual;   // [bs] attended slots (attention over given rows)
 };
 
 // sync (uint32 words, each counter on its own 128-byte line): score count [bs],
@@ -239,7 +242,10 @@ struct HeadSmem {
 // slots, per_wave rows per wave in steps of 32 (kHeadDepth in flight), the
 // waves combined in LDS.  With one part the block writes the output; else it
 // stores an (m, l, o) partial (agent scope) and the block that completes the
-// (request, KV head) count merges the parts.
+// (request, KV head) count merges the parts.  ROWS: the pool rows of the slots
+// are given (rows_in, actual) instead of coming from the page list and
+// req_to_token - the same arithmetic over the same slot order.
+template <bool ROWS>
 __global__ __launch_bounds__(64 * kHeadWaves, 1) void quest_attend_part_kernel(StepArgs a) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   HeadSmem& sm = *reinterpret_cast<HeadSmem*>(smem_raw);
@@ -252,25 +258,31 @@ __global__ __launch_bounds__(64 * kHeadWaves, 1) void quest_attend_part_kernel(S
   const int parts = a.parts;
   const int bh = blockIdx.x / parts, part = blockIdx.x - bh * parts;
   const int b = bh / kStepKV, h = bh - b * kStepKV;
-  const int64_t s = sa.seq[b];
-  const int64_t req = sa.rpi[b];
+  const int64_t s = ROWS ? 0 : sa.seq[b];
+  const int64_t req = ROWS ? 0 : sa.rpi[b];
   const int top_k = sa.top_k, P = sa.P, k = sa.k_sel;
-  const bool long_b = needs_selection(sa, s);
-  const int n = (int)min(max(s, (int64_t)0), (int64_t)top_k);  // actual_lens (quest.py:345)
-  const bool r2t_ok = req >= 0 && req < a.r2t_rows;
+  const bool long_b = !ROWS && needs_selection(sa, s);
+  // actual_lens (quest.py:345)
+  const int n = ROWS ? min(max(a.actual[b], 0), top_k) : (int)min(max(s, (int64_t)0), (int64_t)top_k);
+  const bool r2t_ok = !ROWS && req >= 0 && req < a.r2t_rows;
   // slots [slot_base, slot_base + per_block): per_wave rows per wave, a multiple of
   // the 32-row step; the row table is filled over the whole range (row 0 past n),
   // so every row a step reads is initialised and in range
   const int per_wave = a.per_wave;
   const int per_block = kHeadWaves * per_wave;  // <= kStepMaxTopK
   const int slot_base = part * per_block;
-  int32_t* pos_out = h == 0 ? sa.positions + (int64_t)b * top_k : nullptr;
+  int32_t* pos_out = !ROWS && h == 0 ? sa.positions + (int64_t)b * top_k : nullptr;
   for (int i0 = 0; i0 < per_block; i0 += kThreads * 4) {
     int64_t pv[4];
-    int32_t rv[4];
+    int64_t rv[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int slot = slot_base + i0 + tid + kThreads * u;
+      if (ROWS) {
+        pv[u] = 0;
+        rv[u] = slot < n ? a.rows_in[(int64_t)b * a.rows_stride + slot] : 0;
+        continue;
+      }
       int64_t p;
       if (!long_b)
         p = s <= top_k ? min((int64_t)slot, max(s - 1, (int64_t)0)) : min(max(s - P, (int64_t)0) + slot, s - 1);
@@ -443,16 +455,84 @@ static int device_cu_count() {
   return cached[dev];
 }
 
-// LDS of the attention kernel (above the 64 KiB default: opted in once per device).
+// LDS of the attention kernels (above the 64 KiB default: opted in once per device).
 static size_t head_smem_bytes() {
   static bool opted[64] = {false};
   int dev = 0;
   if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64 && !opted[dev]) {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&quest_attend_part_kernel),
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&quest_attend_part_kernel<false>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)sizeof(HeadSmem));
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&quest_attend_part_kernel<true>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)sizeof(HeadSmem));
     opted[dev] = true;
   }
   return sizeof(HeadSmem);
+}
+
+// Shapes the fused layer step takes (bf16, KV*D = 4*128, G <= 16, page 64, at
+// most 64 selected pages, top_k <= 4096, at most 6144 pages per request).
+// new_dtype < 0: no new token.
+static bool fused_shape(int q_dtype, int kv_dtype, int new_dtype, int num_q_heads, int kv_heads, int head_dim,
+                        int page_size, int top_k, int max_pages) {
+  if (kv_heads != kStepKV || head_dim != kMfmaDim || num_q_heads % kv_heads != 0 || page_size != 64 ||
+      top_k <= 0 || top_k % page_size != 0)
+    return false;
+  return q_dtype == QQ_DTYPE_BF16 && kv_dtype == QQ_DTYPE_BF16 && (new_dtype < 0 || new_dtype == QQ_DTYPE_BF16) &&
+         num_q_heads / kv_heads <= kStepMaxG && top_k / page_size - 1 <= kMaxSelFused && top_k <= kStepMaxTopK &&
+         max_pages <= 24 * kBlock;
+}
+
+// Attention blocks per (request, KV head) of the fused attention: enough to
+// cover every CU once (the blocks run one per CU), at least 32 rows per wave.
+static int step_parts(int bs, int kv_heads, int top_k) {
+  return max(1, min(kMaxParts, min(device_cu_count() / max(1, bs * kv_heads), ceil_div(top_k, kHeadWaves * 32))));
+}
+
+extern "C" int qq_quest_fused_step(int q_dtype, int kv_dtype, int new_dtype, int num_q_heads, int kv_heads,
+                                   int head_dim, int page_size, int top_k, int max_pages) {
+  return fused_shape(q_dtype, kv_dtype, new_dtype, num_q_heads, kv_heads, head_dim, page_size, top_k, max_pages)
+             ? 1
+             : 0;
+}
+
+// The fused attention over given rows (one launch of quest_attend_part_kernel<true>);
+// QQ_OK when launched, 1 when the shape or the buffers do not allow it.
+int qq::attend_rows_fused(const void* q, int64_t q_bstride, int num_q_heads, const void* k_layer, const void* v_layer,
+                      int64_t kv_rows, const int64_t* rows, int64_t slots, const int32_t* actual, int bs, float scale,
+                      void* out, void* workspace, int64_t workspace_bytes, void* sync, int64_t sync_bytes,
+                      hipStream_t s) {
+  if (!sync || sync_bytes < qq_quest_layer_step_sync_bytes(bs, kStepKV) || slots <= 0 || slots > kStepMaxTopK ||
+      num_q_heads % kStepKV != 0 || num_q_heads / kStepKV > kStepMaxG || !workspace)
+    return 1;
+  const int top_k = (int)slots;
+  const int G = num_q_heads / kStepKV;
+  const int parts = step_parts(bs, kStepKV, top_k);
+  const int64_t part_bytes = (int64_t)bs * kStepKV * parts * G * (kMfmaDim + 2) * (int64_t)sizeof(float);
+  if (parts > 1 && workspace_bytes < part_bytes) return 1;
+  StepArgs a{};
+  a.s.q = q;
+  a.s.q_dtype = QQ_DTYPE_BF16;
+  a.s.q_bstride = q_bstride;
+  a.s.H = num_q_heads;
+  a.s.top_k = top_k;
+  a.s.P = 64;
+  a.k = static_cast<const uint16_t*>(k_layer);
+  a.v = static_cast<const uint16_t*>(v_layer);
+  a.kv_rows = kv_rows;
+  a.sl2 = scale * kLog2e;
+  a.out = static_cast<uint16_t*>(out);
+  a.part_o = static_cast<float*>(workspace);
+  a.part_ml = a.part_o + (int64_t)bs * kStepKV * parts * G * kMfmaDim;
+  a.parts = parts;
+  a.per_wave = ceil_div(top_k, parts * kHeadWaves * 32) * 32;
+  a.sync = static_cast<uint32_t*>(sync);
+  a.bs = bs;
+  a.G = G;
+  a.rows_in = rows;
+  a.rows_stride = slots;
+  a.actual = actual;
+  quest_attend_part_kernel<true><<<bs * kStepKV * parts, 64 * kHeadWaves, head_smem_bytes(), s>>>(a);
+  return QQ_OK;
 }
 
 static int forward_decode(
@@ -515,18 +595,13 @@ static int forward_decode(
 
   const int G = num_q_heads / kv_heads;
   const int64_t pages_bytes = (int64_t)bs * kMaxSelFused * (int64_t)sizeof(int32_t);
-  // attention blocks per (request, KV head): enough to cover every CU once (the
-  // blocks run one per CU), at least 32 rows per wave
-  const int parts = max(1, min(kMaxParts, min(device_cu_count() / max(1, bs * kv_heads),
-                                              ceil_div(top_k, kHeadWaves * 32))));
+  const int parts = step_parts(bs, kv_heads, top_k);
   const int per_wave = ceil_div(top_k, parts * kHeadWaves * 32) * 32;
   const int64_t part_bytes = (int64_t)bs * kv_heads * parts * G * (kMfmaDim + 2) * (int64_t)sizeof(float);
   const bool fused = sync && sync_bytes >= qq_quest_layer_step_sync_bytes(bs, kv_heads) &&
-                     q_dtype == QQ_DTYPE_BF16 && kv_dtype == QQ_DTYPE_BF16 &&
-                     (!k_new || new_dtype == QQ_DTYPE_BF16) && kv_heads == kStepKV &&
-                     head_dim == kMfmaDim && G <= kStepMaxG && page_size == 64 && k_sel <= kMaxSelFused &&
-                     top_k <= kStepMaxTopK && max_pages <= 16 * kBlock && workspace &&
-                     workspace_bytes >= pages_bytes + (parts > 1 ? part_bytes : 0);
+                     fused_shape(q_dtype, kv_dtype, k_new ? new_dtype : -1, num_q_heads, kv_heads, head_dim,
+                                 page_size, top_k, max_pages) &&
+                     workspace && workspace_bytes >= pages_bytes + (parts > 1 ? part_bytes : 0);
   if (fused) {
     StepArgs a;
     a.s = sa;
@@ -557,9 +632,12 @@ static int forward_decode(
       quest_score_select_kernel<8><<<score_blocks, kBlock, 0, s>>>(a);
     else if (n_max <= 12 * kBlock)
       quest_score_select_kernel<12><<<score_blocks, kBlock, 0, s>>>(a);
-    else
+    else if (n_max <= 16 * kBlock)
       quest_score_select_kernel<16><<<score_blocks, kBlock, 0, s>>>(a);
-    if (phase & 2) quest_attend_part_kernel<<<bs * kStepKV * parts, 64 * kHeadWaves, head_smem_bytes(), s>>>(a);
+    else
+      quest_score_select_kernel<24><<<score_blocks, kBlock, 0, s>>>(a);
+    if (phase & 2)
+      quest_attend_part_kernel<false><<<bs * kStepKV * parts, 64 * kHeadWaves, head_smem_bytes(), s>>>(a);
     return check_launch(what);
   }
 

@@ -66,4 +66,12 @@ int launch_score(const SelectArgs& a, int bs, bool store_new, hipStream_t stream
 int launch_attention(AttnArgs& a, int kv_dtype, int bs, int64_t workspace_bytes, void* workspace,
                      hipStream_t stream, const char* what);
 
+// The fused layer step's attention kernel over given rows (`slots` per request,
+// rows[b * slots + i]); QQ_OK when launched, 1 when the shape or the buffers do
+// not allow it.  Callers check bf16 and KV * D = 4 * 128.
+int attend_rows_fused(const void* q, int64_t q_bstride, int num_q_heads, const void* k_layer, const void* v_layer,
+                      int64_t kv_rows, const int64_t* rows, int64_t slots, const int32_t* actual, int bs, float scale,
+                      void* out, void* workspace, int64_t workspace_bytes, void* sync, int64_t sync_bytes,
+                      hipStream_t s);
+
 }  // namespace qq

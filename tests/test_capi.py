@@ -102,3 +102,20 @@ def test_forward_decode_phase_is_validated_without_gpu(lib):
         assert st == _lib.QQ_EINVAL and b"phase" in lib.qq_last_error()
     assert lib.qq_quest_layer_step_sync_bytes(16, 4) == 16 * (1 + 4) * 128
     assert lib.qq_quest_layer_step_sync_bytes(0, 4) == 0
+
+
+def test_fused_step_predicate_without_gpu(lib):
+    """qq_quest_fused_step: the shapes the fused layer step takes (no HIP call)."""
+    from qwenquest_amd import _lib
+
+    bf, f32 = _lib.DTYPE_BF16, _lib.DTYPE_F32
+    # the benchmark shape: 32 q / 4 KV heads x 128, page 64, top_k 2048, 2049 pages
+    assert lib.qq_quest_fused_step(bf, bf, bf, 32, 4, 128, 64, 2048, 2049) == 1
+    assert lib.qq_quest_fused_step(bf, bf, -1, 32, 4, 128, 64, 2048, 6144) == 1  # no new token; 6144 pages
+    assert lib.qq_quest_fused_step(bf, bf, bf, 32, 4, 128, 64, 2048, 6145) == 0  # too many pages
+    assert lib.qq_quest_fused_step(bf, bf, bf, 32, 4, 128, 16, 2048, 2049) == 0  # page 16
+    assert lib.qq_quest_fused_step(bf, bf, bf, 32, 4, 128, 64, 4224, 2049) == 0  # 65 selected pages
+    assert lib.qq_quest_fused_step(bf, bf, f32, 32, 4, 128, 64, 2048, 2049) == 0  # fp32 new token
+    assert lib.qq_quest_fused_step(f32, bf, bf, 32, 4, 128, 64, 2048, 2049) == 0  # fp32 queries
+    assert lib.qq_quest_fused_step(bf, bf, bf, 16, 2, 128, 64, 2048, 2049) == 0  # 2 KV heads
+    assert lib.qq_quest_fused_step(bf, bf, bf, 128, 4, 128, 64, 2048, 2049) == 0  # G = 32

@@ -9,6 +9,7 @@ import pytest
 import torch
 
 from oracle import hisparse as oh
+from qwenquest_amd import _lib
 from tests.conftest import load_golden
 
 pytestmark = pytest.mark.gpu
@@ -208,29 +209,38 @@ def test_golden_200_step_trace_through_the_kernels():
     assert [s.hits, s.misses] == g["stats"][-1].tolist()
 
 
+# (q heads, kv heads, head_dim, top_k, page, hot buffer, ctx, prompts, steps).  The last
+# shape is the fused layer step's (32/4/128, page 64): quest runs the fused two-launch step,
+# quest_hisparse the same attention kernel over its hot-buffer rows.
+BIT_IDENTITY = [
+    (8, 2, 16, 32, 8, 48, 256, {0: 90, 1: 107}, 60),
+    (16, 2, 128, 32, 8, 48, 256, {0: 90, 1: 107}, 60),
+    (32, 4, 128, 256, 64, 384, 1200, {0: 700, 1: 1003}, 40),
+]
+
+
 @pytest.mark.parametrize("avoid", [False, True])
-@pytest.mark.parametrize("H,KVH,DIM", [(8, 2, 16), (16, 2, 128)])
-def test_quest_hisparse_is_bit_identical_to_quest(avoid, H, KVH, DIM):
+@pytest.mark.parametrize("shape", range(len(BIT_IDENTITY)))
+def test_quest_hisparse_is_bit_identical_to_quest(avoid, shape):
     """reference tests/test_engine.py:59-69 and test_bf16.py:27-43 at the backend boundary:
     the same q/k/v through QuestOnlyBackend and QuestHiSparseBackend over many decode steps
-    (the hot buffer must swap) give bit-identical outputs.  head_dim 128 runs the
-    merge-free kernel in both modes (selection fused in quest, rows given in hisparse)."""
+    (the hot buffer must swap) give bit-identical outputs and positions, also where quest
+    runs the fused layer step."""
     from qwenquest_amd.attention.quest_hisparse import QuestHiSparseBackend
     from qwenquest_amd.attention.quest_only import QuestOnlyBackend
     from qwenquest_amd.batch import ForwardBatch, ForwardMode
     from qwenquest_amd.memory import MHATokenToKVPool, ReqToTokenPool
 
-    L, CTX = 3, 256
-    cfg = {"algorithm": "quest", "top_k": 32, "quest_page_size": 8, "device_buffer_size": 48,
+    H, KVH, DIM, TOP_K, P, BUF, CTX, prompts, steps = BIT_IDENTITY[shape]
+    L = 3
+    cfg = {"algorithm": "quest", "top_k": TOP_K, "quest_page_size": P, "device_buffer_size": BUF,
            "avoid_recent_overlap": avoid}
     gen = torch.Generator().manual_seed(3)
-    prompts = {0: 90, 1: 107}
-    steps = 60
     total = max(prompts.values()) + steps + 1
     kk = torch.randn(L, 2, total, KVH, DIM, generator=gen).to(torch.bfloat16)
     vv = torch.randn(L, 2, total, KVH, DIM, generator=gen).to(torch.bfloat16)
     qq = torch.randn(steps, L, 2, H, DIM, generator=gen).to(torch.bfloat16)
-    outs = {}
+    outs, poss = {}, {}
     for mode in ("quest", "quest_hisparse"):
         rtp = ReqToTokenPool(2, CTX, DEV)
         kvp = MHATokenToKVPool(2 * CTX, L, KVH, DIM, torch.bfloat16, DEV)
@@ -254,7 +264,7 @@ def test_quest_hisparse_is_bit_identical_to_quest(avoid, H, KVH, DIM):
             def __init__(self, i):
                 self.layer_id, self.scaling = i, DIM**-0.5
 
-        res = []
+        res, pos = [], []
         for step in range(steps):
             seqs = [prompts[r] + step + 1 for r in (0, 1)]
             locs = torch.tensor([1 + r * CTX + s - 1 for r, s in zip((0, 1), seqs)], device=DEV)
@@ -265,8 +275,13 @@ def test_quest_hisparse_is_bit_identical_to_quest(avoid, H, KVH, DIM):
                 kn = torch.stack([kk[layer, r, s - 1] for r, s in zip((0, 1), seqs)]).to(DEV)
                 vn = torch.stack([vv[layer, r, s - 1] for r, s in zip((0, 1), seqs)]).to(DEV)
                 res.append(be.forward_decode(qq[step, layer].to(DEV), kn, vn, Layer(layer), b).cpu())
-        outs[mode] = torch.stack(res)
+                pos.append(be._positions[:2].cpu())
+        outs[mode], poss[mode] = torch.stack(res), torch.stack(pos)
         if mode == "quest_hisparse":
             st = be.coord.stats
             assert st.misses > 0 and st.hits > 0
+    fused = _lib.load().qq_quest_fused_step(_lib.DTYPE_BF16, _lib.DTYPE_BF16, _lib.DTYPE_BF16, H, KVH, DIM, P, TOP_K,
+                                            (CTX + P - 1) // P)
+    assert fused == (shape == len(BIT_IDENTITY) - 1)
+    assert torch.equal(poss["quest"], poss["quest_hisparse"])
     assert torch.equal(outs["quest"], outs["quest_hisparse"])
