@@ -87,27 +87,38 @@ def time_graph(fn, reps: int, stream) -> float:
     return start.elapsed_time(end) / (3 * reps)
 
 
-def cpu_baseline(top_k, page, heads, kv, dim, ctx, sample_reqs: int) -> dict:
-    """The oracle (numpy, one core) on `sample_reqs` requests of one layer at full context."""
+def cpu_baseline(top_k, page, heads, kv, dim, ctx, sample_reqs: int, seconds: float) -> dict:
+    """The oracle (numpy, BLAS held to one thread) on one layer of `sample_reqs` generated
+    requests at full context, evaluated over and over (a fresh query each time) for about
+    `seconds` of CPU time; the median time per request-layer."""
+    from threadpoolctl import threadpool_limits
+
     from oracle import attention as oa
     from oracle import bf16
     from oracle import quest as oq
 
     rng = np.random.default_rng(7)
     n_pages = ctx // page
-    times = []
+    reqs = []
     for _ in range(sample_reqs):
         bounds = bf16.from_f32(np.sort(rng.standard_normal((n_pages, kv, dim, 2), dtype=np.float32), axis=-1))
         k = bf16.round_f32(rng.standard_normal((ctx, kv, dim), dtype=np.float32))
         v = bf16.round_f32(rng.standard_normal((ctx, kv, dim), dtype=np.float32))
-        q = bf16.round_f32(rng.standard_normal((1, heads, dim), dtype=np.float32))
-        t0 = time.perf_counter()
-        qbar = oq.group_queries(q, kv, dim, is_bf16=True)
-        lay = oq.step_layout([ctx], page, top_k, False)
-        pos, actual, _ = oq.retrieve_topk(qbar, bounds[None], lay, page, top_k)
-        oa.sparse_decode(q, k, v, [pos[0, : int(actual[0])]], dim**-0.5)
-        times.append(time.perf_counter() - t0)
-    return {"per_request_s": float(np.median(times)), "reqs": sample_reqs}
+        reqs.append((bounds, k, v))
+    times = []
+    with threadpool_limits(limits=1):
+        t_end = time.perf_counter() + seconds
+        while len(times) < 3 or time.perf_counter() < t_end:
+            bounds, k, v = reqs[len(times) % sample_reqs]
+            q = bf16.round_f32(rng.standard_normal((1, heads, dim), dtype=np.float32))
+            t0 = time.perf_counter()
+            qbar = oq.group_queries(q, kv, dim, is_bf16=True)
+            lay = oq.step_layout([ctx], page, top_k, False)
+            pos, actual, _ = oq.retrieve_topk(qbar, bounds[None], lay, page, top_k)
+            oa.sparse_decode(q, k, v, [pos[0, : int(actual[0])]], dim**-0.5)
+            times.append(time.perf_counter() - t0)
+    return {"per_request_s": float(np.median(times)), "reqs": sample_reqs, "evaluations": len(times),
+            "cpu_s": float(np.sum(times))}
 
 
 def pinned_h2d_peak(nbytes: int = 1 << 30, reps: int = 5) -> float:
@@ -230,6 +241,7 @@ def main() -> int:
     ap.add_argument("--layers", type=int, default=48)
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--cpu-sample", type=int, default=2, help="requests in the CPU-baseline sample (0 = skip)")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU time the baseline sample runs for")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB three times (scale for the HBM byte counters)")
     ap.add_argument("--hisparse", action="store_true", help="measure the quest_hisparse tier instead")
@@ -351,11 +363,12 @@ def main() -> int:
     cpu = None
     if args.cpu_sample > 0:
         cores = 1
-        c = cpu_baseline(TOP_K, P, H, KV, D, S, args.cpu_sample)
+        c = cpu_baseline(TOP_K, P, H, KV, D, S, args.cpu_sample, args.cpu_seconds)
         us_cpu = c["per_request_s"] * B * 1e6
         cpu = {"value": round(us_cpu, 1), "unit": "us per layer-step", "cores": cores, "kind": "port",
-               "sample": f"numpy oracle, {args.cpu_sample} requests x 1 layer at {S} tokens "
-                         f"(score+select+gather+attention), median per request x {B}"}
+               "sample": f"numpy oracle (one thread), {c['evaluations']} request-layer evaluations "
+                         f"({c['cpu_s']:.1f} s) over {args.cpu_sample} generated requests at {S} tokens "
+                         f"(GQA mean + scores + top-k + gather + attention); median per request x {B}"}
 
     line = {
         "metric": "µs per Quest decode layer-step @128K ctx, batch 16; % peak HBM BW",
