@@ -196,12 +196,15 @@ __global__ __launch_bounds__(kPlanThreads) void swap_plan_kernel(SwapArgs a) {
   __syncthreads();
 
   // misses: first occurrences without a hit, ranked in entry order (entry i = tid + k*1024
-  // is not contiguous per thread, so rank by a scan per k-round)
+  // is not contiguous per thread, so rank by a scan per k-round; rounds past n hold none)
+  const int rounds = (n + kPlanThreads - 1) / kPlanThreads;
   int uniq_local = 0;
   int miss_rank[kMaxPerThread];
   int num_miss = 0;
 #pragma unroll
   for (int k = 0; k < kMaxPerThread; ++k) {
+    miss_rank[k] = -1;
+    if (k >= rounds) continue;  // block-uniform
     const bool miss = my_first[k] && s_val[my_h[k] >= 0 ? my_h[k] : 0] < 0;
     uniq_local += my_first[k] ? 1 : 0;
     int tot;
