@@ -130,6 +130,117 @@ __global__ __launch_bounds__(kThreads) void prefill_bounds_kernel(PrefillArgs a)
   }
 }
 
+// bf16 keys with KV*D = C a power of two in [8, 2048]: the same fold with
+// 16-byte loads.  L = C / 8 lanes cover a row (8 channels each), the block's
+// kThreads / L row groups take contiguous runs of the chunk's rows, and the
+// groups' results fold in group order - the rows are folded in their order,
+// as above (ties and NaNs resolve as in a sequential fold).
+template <int L>
+__global__ __launch_bounds__(kThreads) void prefill_bounds_wide_kernel(PrefillArgs a) {
+  constexpr int kGroups = kThreads / L;
+  constexpr int C = L * 8;
+  const int64_t page = blockIdx.x;
+  const int li = blockIdx.y;
+  const int layer = a.layer_begin + li;
+  const int64_t begin = page * a.P;
+  const int64_t end = min(begin + (int64_t)a.P, a.n);
+  if (a.set_counters && page == 0 && li == a.n_layers - 1 && threadIdx.x == 0) {
+    a.count[a.req] = (int32_t)(a.n - a.full_pages * a.P);
+    a.page_idx[a.req] = (int32_t)a.full_pages;
+  }
+  if (begin >= end) return;
+  const uint4* kl = reinterpret_cast<const uint4*>(a.k_base + (int64_t)li * a.k_layer_stride_bytes);
+  __shared__ int64_t s_rows[kRowChunk];
+  __shared__ uint4 s_mn[kGroups][L], s_mx[kGroups][L];
+  const int lane = threadIdx.x % L, grp = threadIdx.x / L;
+  uint16_t mn[8], mx[8];  // the block's fold so far (kept by group 0)
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    mn[e] = 0x7F80;
+    mx[e] = 0xFF80;
+  }
+  for (int64_t t0 = begin; t0 < end; t0 += kRowChunk) {
+    const int cnt = (int)min((int64_t)kRowChunk, end - t0);
+    __syncthreads();
+    for (int t = threadIdx.x; t < cnt; t += kThreads) {
+      const int64_t row = load_index(a.idx, a.idx64, t0 + t);
+      s_rows[t] = (row >= 0 && row < a.k_rows) ? row : -1;
+    }
+    __syncthreads();
+    // group grp folds rows [r0, r1) of the chunk
+    const int per = (cnt + kGroups - 1) / kGroups;
+    const int r0 = min(cnt, grp * per), r1 = min(cnt, r0 + per);
+    uint16_t gmn[8], gmx[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      gmn[e] = 0x7F80;
+      gmx[e] = 0xFF80;
+    }
+#pragma unroll 4
+    for (int t = r0; t < r1; ++t) {
+      const int64_t row = s_rows[t];
+      if (row < 0) continue;
+      const uint4 v = kl[row * (C / 8) + lane];
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint16_t x = (uint16_t)(w[e >> 1] >> ((e & 1) * 16));
+        gmn[e] = bmin(gmn[e], x);
+        gmx[e] = bmax(gmx[e], x);
+      }
+    }
+    uint4 pm, px;
+    pm.x = gmn[0] | ((uint32_t)gmn[1] << 16);
+    pm.y = gmn[2] | ((uint32_t)gmn[3] << 16);
+    pm.z = gmn[4] | ((uint32_t)gmn[5] << 16);
+    pm.w = gmn[6] | ((uint32_t)gmn[7] << 16);
+    px.x = gmx[0] | ((uint32_t)gmx[1] << 16);
+    px.y = gmx[2] | ((uint32_t)gmx[3] << 16);
+    px.z = gmx[4] | ((uint32_t)gmx[5] << 16);
+    px.w = gmx[6] | ((uint32_t)gmx[7] << 16);
+    s_mn[grp][lane] = pm;
+    s_mx[grp][lane] = px;
+    __syncthreads();
+    if (grp == 0) {
+#pragma unroll
+      for (int g = 0; g < kGroups; ++g) {
+        const uint4 qm = s_mn[g][lane], qx = s_mx[g][lane];
+        const uint32_t wm[4] = {qm.x, qm.y, qm.z, qm.w}, wx[4] = {qx.x, qx.y, qx.z, qx.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          mn[e] = bmin(mn[e], (uint16_t)(wm[e >> 1] >> ((e & 1) * 16)));
+          mx[e] = bmax(mx[e], (uint16_t)(wx[e >> 1] >> ((e & 1) * 16)));
+        }
+      }
+    }
+  }
+  if (grp != 0) return;
+  const int c0 = lane * 8;
+  const int64_t rc = ((int64_t)layer * a.R + a.req) * C + c0;
+  if (page < a.full_pages) {
+    if (page < a.MP) {
+      uint32_t* dst = a.bounds + (((int64_t)layer * a.R + a.req) * a.MP + page) * C + c0;
+      uint4 lo, hi;
+      lo.x = pack_pair(mn[0], mx[0]);
+      lo.y = pack_pair(mn[1], mx[1]);
+      lo.z = pack_pair(mn[2], mx[2]);
+      lo.w = pack_pair(mn[3], mx[3]);
+      hi.x = pack_pair(mn[4], mx[4]);
+      hi.y = pack_pair(mn[5], mx[5]);
+      hi.z = pack_pair(mn[6], mx[6]);
+      hi.w = pack_pair(mn[7], mx[7]);
+      reinterpret_cast<uint4*>(dst)[0] = lo;
+      reinterpret_cast<uint4*>(dst)[1] = hi;
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      a.rmin[rc + e] = mn[e];
+      a.rmax[rc + e] = mx[e];
+    }
+  }
+}
+
 struct DecodeArgs {
   const char* k_base;
   int64_t k_layer_stride_bytes;
@@ -323,7 +434,30 @@ extern "C" int qq_quest_prefill_bounds(const void* k_base, int64_t k_layer_strid
   a.full_pages = full;
   const int pages = max(1, ceil_div(n_tokens, page_size));
   dim3 grid(pages, n_layers);
-  prefill_bounds_kernel<<<grid, kThreads, 0, static_cast<hipStream_t>(stream)>>>(a);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int C = a.C;
+  const bool wide = k_dtype == QQ_DTYPE_BF16 && C >= 8 && C <= 8 * kThreads && (C & (C - 1)) == 0 &&
+                    k_layer_stride % 8 == 0 && reinterpret_cast<uintptr_t>(k_base) % 16 == 0;
+  if (!wide)
+    prefill_bounds_kernel<<<grid, kThreads, 0, s>>>(a);
+  else if (C == 512)
+    prefill_bounds_wide_kernel<64><<<grid, kThreads, 0, s>>>(a);
+  else if (C == 1024)
+    prefill_bounds_wide_kernel<128><<<grid, kThreads, 0, s>>>(a);
+  else if (C == 2048)
+    prefill_bounds_wide_kernel<256><<<grid, kThreads, 0, s>>>(a);
+  else if (C == 256)
+    prefill_bounds_wide_kernel<32><<<grid, kThreads, 0, s>>>(a);
+  else if (C == 128)
+    prefill_bounds_wide_kernel<16><<<grid, kThreads, 0, s>>>(a);
+  else if (C == 64)
+    prefill_bounds_wide_kernel<8><<<grid, kThreads, 0, s>>>(a);
+  else if (C == 32)
+    prefill_bounds_wide_kernel<4><<<grid, kThreads, 0, s>>>(a);
+  else if (C == 16)
+    prefill_bounds_wide_kernel<2><<<grid, kThreads, 0, s>>>(a);
+  else
+    prefill_bounds_wide_kernel<1><<<grid, kThreads, 0, s>>>(a);
   return check_launch("qq_quest_prefill_bounds");
 }
 
