@@ -17,6 +17,7 @@ rocprofv3 PMC summary in profiles/ (copy-calibrated FETCH_SIZE + WRITE_SIZE).
 
     python bench.py [--steps K] [--warmup W]
 
+`--ragged` draws each request's context uniform in [8192, ctx] (seeded) instead.
 `--hisparse` measures the quest_hisparse tier instead (batch 16, 128K context,
 a hot buffer of 4096 + 1 rows per request and layer, the full K/V history in
 pinned host memory, queries AR(1) with rho 0.9 across steps): swap-in rows per
@@ -244,6 +245,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU time the baseline sample runs for")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB three times (scale for the HBM byte counters)")
+    ap.add_argument("--ragged", action="store_true",
+                    help="contexts drawn uniform in [8192, ctx] per request (seeded) instead of all ctx")
     ap.add_argument("--hisparse", action="store_true", help="measure the quest_hisparse tier instead")
     ap.add_argument("--hisparse-layers", type=int, default=4)
     args = ap.parse_args()
@@ -275,8 +278,13 @@ def main() -> int:
     B, S, L = args.batch, args.ctx, args.layers
     H, KV, D, P, TOP_K = 32, 4, 128, 64, 2048
     total_steps = args.warmup + args.steps + 2
-    max_ctx = S + total_steps + 64
-    rows = B * max_ctx
+    ctxs = (np.random.default_rng(2024).integers(8192, S, size=B, endpoint=True) if args.ragged
+            else np.full(B, S, dtype=np.int64))
+    max_ctx = int(ctxs.max()) + total_steps + 64
+    # request r's rows follow r-1's: its context plus room for the decode steps
+    span = ctxs + total_steps + 64
+    starts = 1 + np.concatenate([[0], np.cumsum(span)[:-1]])
+    rows = int(span.sum())
 
     t_setup = time.perf_counter()
     rtp = ReqToTokenPool(B, max_ctx, dev)
@@ -285,19 +293,19 @@ def main() -> int:
     for layer in range(L):
         kvp.k_all[layer].normal_(generator=gen)
         kvp.v_all[layer].normal_(generator=gen)
-    base = 1 + torch.arange(B, device=dev, dtype=torch.int64) * max_ctx
-    rtp.req_to_token.copy_((base[:, None] + torch.arange(max_ctx, device=dev)[None]).to(torch.int32))
+    base = torch.tensor(starts, device=dev, dtype=torch.int64)
+    rtp.req_to_token.copy_((base[:, None] + torch.arange(max_ctx, device=dev)[None]).clamp(max=rows).to(torch.int32))
     be = QuestOnlyBackend(rtp, kvp, {"algorithm": "quest", "top_k": TOP_K, "quest_page_size": P})
-    prompt = S - 1  # prefill covers positions [0, S-1); the first decode step has seq_len S
     for r in range(B):
-        be.quest.update_prefill_representations_fused(r, kvp.k_all, rtp.req_to_token[r, :prompt])
+        # prefill covers positions [0, ctx - 1); the first decode step has seq_len ctx
+        be.quest.update_prefill_representations_fused(r, kvp.k_all, rtp.req_to_token[r, : int(ctxs[r]) - 1])
         be._skip_first_decode_update[r] = True
     q_all = torch.randn((L, B, H, D), generator=gen, device=dev).to(torch.bfloat16)
     k_new = torch.randn((L, B, KV, D), generator=gen, device=dev).to(torch.bfloat16)
     v_new = torch.randn((L, B, KV, D), generator=gen, device=dev).to(torch.bfloat16)
     layers = [Layer(i, D**-0.5) for i in range(L)]
     rpi = torch.arange(B, device=dev, dtype=torch.int64)
-    seq_lens = torch.full((B,), S, device=dev, dtype=torch.int64)
+    seq_lens = torch.tensor(ctxs, device=dev, dtype=torch.int64)
     out_loc = torch.empty(B, device=dev, dtype=torch.int64)
     torch.cuda.synchronize()
     setup_s = time.perf_counter() - t_setup
@@ -332,7 +340,7 @@ def main() -> int:
     ms_per_step = elapsed * 1e3 / args.steps
     us_per_layer_step = ms_per_step * 1e3 / L
 
-    seqs_timed = [S + 1 + args.warmup + args.steps // 2] * B
+    seqs_timed = [int(c) + 1 + args.warmup + args.steps // 2 for c in ctxs]
     byts = algorithmic_bytes(seqs_timed, P, TOP_K, 2 * KV * D * 2, KV * D * 2 * 2)
     step_frac = byts["headline"] / (us_per_layer_step * 1e-6) / (HBM_PEAK_GBS * 1e9)
 
@@ -361,7 +369,7 @@ def main() -> int:
         "quest_score_select_kernel", ms_sel, byts["bounds"], bw_sel)
 
     cpu = None
-    if args.cpu_sample > 0:
+    if args.cpu_sample > 0 and not args.ragged:
         cores = 1
         c = cpu_baseline(TOP_K, P, H, KV, D, S, args.cpu_sample, args.cpu_seconds)
         us_cpu = c["per_request_s"] * B * 1e6
@@ -370,8 +378,11 @@ def main() -> int:
                          f"({c['cpu_s']:.1f} s) over {args.cpu_sample} generated requests at {S} tokens "
                          f"(GQA mean + scores + top-k + gather + attention); median per request x {B}"}
 
+    ctx_desc = (f"contexts uniform in [8192, {S}] (seeded, mean {int(ctxs.mean())})" if args.ragged
+                else f"{S}-token context")
     line = {
-        "metric": "µs per Quest decode layer-step @128K ctx, batch 16; % peak HBM BW",
+        "metric": ("µs per Quest decode layer-step, ragged contexts, batch 16; % peak HBM BW" if args.ragged
+                   else "µs per Quest decode layer-step @128K ctx, batch 16; % peak HBM BW"),
         "value": round(us_per_layer_step, 2),
         "unit": "us per layer-step",
         "n_gpus": 1,
@@ -383,9 +394,9 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic N(0,1) q/k/v, fixed seeds",
-        "config": {"workload": f"quest decode, batch {B}, {S}-token context, {L} layers, "
+        "config": {"workload": f"quest decode, batch {B}, {ctx_desc}, {L} layers, "
                                f"32q/4kv heads x 128, page 64, top_k 2048",
-                   "batch": B, "seq_len": S, "layers": L, "graph": not args.no_graph},
+                   "batch": B, "seq_len": S, "layers": L, "graph": not args.no_graph, "ragged": bool(args.ragged)},
         "hbm_frac_layer_step": round(step_frac, 4),
         "tokens_per_s": round(B / (ms_per_step * 1e-3), 1),
         "algorithmic_bytes_per_layer_step": byts,
@@ -393,7 +404,7 @@ def main() -> int:
                        "quest_attend_part_kernel": round(ms_att * 1e3, 2)},
         "roofline": {"kernel": dominant[0], "bound": "hbm", "achieved": round(dominant[3], 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(dominant[3] / HBM_PEAK_GBS, 4),
-                     "traffic": profiled_traffic().get(dominant[0])},
+                     "traffic": None if args.ragged else profiled_traffic().get(dominant[0])},
         "cpu_baseline": cpu,
         "setup_s": round(setup_s, 1),
     }

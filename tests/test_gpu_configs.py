@@ -267,3 +267,49 @@ def test_batch4_262k_outliers_quest_and_hisparse(avoid):
                 rows = torch.from_numpy(1 + i * ctx + ref_pos[i, :n].astype(np.int64))
                 ref = oracle_attention(qs[step, i].cpu(), kk[rows], vv[rows])
                 assert np.abs(outs[step, i].float().numpy() - ref).max() < 2e-2, f"step {step} request {i}"
+
+
+def test_batch64_one_part_per_head():
+    """Batch 64 x 8192 tokens: with 64 x 4 (request, KV head) pairs on the CUs the fused
+    attention runs one part per head (no partial merge, 2048 rows per block); positions
+    bit-exact vs the oracle, attention within 2e-2, over 3 decode steps."""
+    from qwenquest_amd.batch import ForwardBatch, ForwardMode
+
+    B, S, steps = 64, 8192, 3
+    ctx = S + steps + 64
+    rtp, kvp, be, base = make_quest_backend(B, ctx, 1)
+    kvp.k_all[0].copy_(dev_randn((B * ctx + 1, KV, D), 31).to(torch.bfloat16))
+    kvp.v_all[0].copy_(dev_randn((B * ctx + 1, KV, D), 32).to(torch.bfloat16))
+    prompt = S - 1
+    for r in range(B):
+        be.quest.update_prefill_representations_fused(r, kvp.k_all, rtp.req_to_token[r, :prompt])
+        be._skip_first_decode_update[r] = True
+    kk, vv = kvp.k_all[0].cpu(), kvp.v_all[0].cpu()
+    kbits = bf16_bits(kk)
+    st = oq.QuestState(TOP_K, P)
+    st.init_storage(0, 1, B, ctx, KV, D)
+    for r in range(B):
+        st.update_prefill_representations(0, r, kbits, 1 + r * ctx + np.arange(prompt))
+    reqs = list(range(B))
+    for step in range(steps):
+        seq = torch.full((B,), S + step, device=DEV, dtype=torch.int64)
+        loc = base + seq - 1
+        batch = ForwardBatch(ForwardMode.DECODE, None, None, torch.arange(B, device=DEV), seq, loc, rtp, kvp, be)
+        be.init_forward_metadata(batch)
+        if step > 0:
+            st.update_decode_representations(0, reqs, kbits, (loc - 1).cpu().numpy())
+            st.maybe_finalize_decode_representations(reqs)
+        st.prepare_step(seq.cpu().numpy())
+        q = dev_randn((B, H, D), 400 + step).to(torch.bfloat16)
+        lc = loc.cpu()
+        out = be.forward_decode(q, kk[lc].to(DEV), vv[lc].to(DEV), Layer(0), batch).float().cpu().numpy()
+        pos = be._positions[:B].cpu().numpy()
+        ref_pos, ref_actual, _ = st.retrieve_topk(q.float().cpu().numpy(), 0, reqs)
+        qc = q.cpu()
+        for i in range(0, B, 7):
+            n = int(ref_actual[i])
+            assert np.array_equal(pos[i, :n], ref_pos[i, :n]), f"step {step} request {i}"
+            rows = torch.from_numpy(1 + i * ctx + ref_pos[i, :n].astype(np.int64))
+            ref = oracle_attention(qc[i], kk[rows], vv[rows])
+            assert np.abs(out[i] - ref).max() < 2e-2, f"step {step} request {i}"
+        assert np.array_equal(pos[:, :TOP_K], ref_pos[:, :TOP_K])
