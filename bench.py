@@ -351,7 +351,7 @@ def main() -> int:
     be.quest.prepare_step(seq_lens)
     turn = {"sel": 0, "att": 0}
 
-    def score_select():
+    def score():
         i = turn["sel"] % L
         turn["sel"] += 1
         be.forward_decode_phase(q_all[i], k_new[i], v_new[i], layers[i], batch, 1)
@@ -361,12 +361,12 @@ def main() -> int:
         turn["att"] += 1
         be.forward_decode_phase(q_all[i], k_new[i], v_new[i], layers[i], batch, 2)
 
-    ms_sel = time_graph(score_select, L, stream)
+    ms_sel = time_graph(score, L, stream)
     ms_att = time_graph(attend, L, stream)
     bw_sel = byts["bounds"] / (ms_sel * 1e-3) / 1e9
     bw_att = byts["kv"] / (ms_att * 1e-3) / 1e9
     dominant = ("quest_attend_part_kernel", ms_att, byts["kv"], bw_att) if ms_att >= ms_sel else (
-        "quest_score_select_kernel", ms_sel, byts["bounds"], bw_sel)
+        "score_pages_fast_kernel", ms_sel, byts["bounds"], bw_sel)
 
     cpu = None
     if args.cpu_sample > 0 and not args.ragged:
@@ -400,7 +400,7 @@ def main() -> int:
         "hbm_frac_layer_step": round(step_frac, 4),
         "tokens_per_s": round(B / (ms_per_step * 1e-3), 1),
         "algorithmic_bytes_per_layer_step": byts,
-        "kernels_us": {"quest_score_select_kernel": round(ms_sel * 1e3, 2),
+        "kernels_us": {"score_pages_fast_kernel": round(ms_sel * 1e3, 2),
                        "quest_attend_part_kernel": round(ms_att * 1e3, 2)},
         "roofline": {"kernel": dominant[0], "bound": "hbm", "achieved": round(dominant[3], 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(dominant[3] / HBM_PEAK_GBS, 4),

@@ -181,9 +181,8 @@ int qq_quest_fused_step(int q_dtype, int kv_dtype, int new_dtype, int num_q_head
                         int head_dim, int page_size, int top_k, int max_pages);
 
 /* Bytes of the sync buffer qq_quest_forward_decode's two-launch path uses for
- * `bs` requests (one counter per request and per (request, KV head), each on
- * its own 128-byte line).  The caller zeroes it once; every call leaves it
- * zeroed again. */
+ * `bs` requests (one counter per (request, KV head), each on its own 128-byte
+ * line).  The caller zeroes it once; every call leaves it zeroed again. */
 int64_t qq_quest_layer_step_sync_bytes(int bs, int kv_heads);
 
 /* Replaces QuestOnlyBackend.forward_decode (src/qwenquest/attention/quest_only.py:132-159)
@@ -197,8 +196,9 @@ int64_t qq_quest_layer_step_sync_bytes(int bs, int kv_heads);
  * qq_decode_attention_workspace_bytes(bs, top_k, H, D).
  * With `sync` (>= qq_quest_layer_step_sync_bytes, zeroed before the first
  * call) and the shapes of qq_quest_fused_step (bf16 tensors, KV*D = 4*128,
- * page 64, top_k/P - 1 <= 64, max_pages <= 6144), the layer runs as two launches (score + select, then
- * attention + merge; the selection and the merge hand off inside them);
+ * page 64, top_k/P - 1 <= 64, max_pages <= 6144), the layer runs as two launches (page
+ * scores + new token, then per (request, KV head, part) the request's selection,
+ * layout, attention and the merge of the parts, handed off inside the launch);
  * otherwise, or with sync == NULL, as four launches.  Calls sharing one sync
  * buffer must not overlap (one stream). */
 int qq_quest_forward_decode(const void* q, int q_dtype, int64_t q_batch_stride, int num_q_heads,
@@ -214,9 +214,9 @@ int qq_quest_forward_decode(const void* q, int q_dtype, int64_t q_batch_stride, 
                             int64_t workspace_bytes, void* sync, int64_t sync_bytes, void* stream);
 
 /* qq_quest_forward_decode split into its two stages, for callers that run
- * other work between them or time them separately: phase 1 = scoring +
- * selection and the new token's K/V store, phase 2 = layout + attention
- * (consumes what phase 1 left in `workspace` / `positions`), phase 3 = both.
+ * other work between them or time them separately: phase 1 = page scoring and
+ * the new token's K/V store, phase 2 = selection + layout + attention
+ * (consumes the scores phase 1 left in `scores_ws`), phase 3 = both.
  * `positions` and `out` are complete after phase 2.  Arguments as for
  * qq_quest_forward_decode; no counterpart in the reference. */
 int qq_quest_forward_decode_phase(const void* q, int q_dtype, int64_t q_batch_stride, int num_q_heads,

@@ -5,22 +5,21 @@
 // Fused path (bf16, KV*D = 4*128, page 64, at most 64 selected pages, at most
 // 6144 pages per request, top_k <= 4096, and a zeroed sync buffer from the
 // caller): two launches.
-//   1. score + select, one block per (request, 32 candidate pages), the whole
-//      grid resident at once: 4 waves x 8 pages scored, scores out with
-//      agent-scope stores, then the block counts itself on its request's
-//      counter.  The block that completes the count selects the request's
-//      pages (filter top-k over the scores) and writes the page list, and
-//      stores the new token's K/V (set_kv_buffer, memory.py:114-120).
+//   1. page scores of every long request (score_pages_fast_kernel, one block
+//      per (request, 32 candidate pages), all CUs) and the new token's K/V
+//      (set_kv_buffer, memory.py:114-120).
 //   2. attention, one block per (request, KV head, part of the rows), enough
-//      parts to put one block on every CU: the block turns its share of the
-//      page list into layout positions and pool rows (req_to_token,
+//      parts to put one block on every CU: the block selects its request's
+//      pages from the scores (filter top-k; every block of a request computes
+//      the same list, so no block waits on another), turns its share of the
+//      list into layout positions and pool rows (req_to_token,
 //      quest_only.py:149-151) in LDS - the KV-head-0 blocks also write the
 //      positions - then each of its 8 waves streams its rows in steps of 32
 //      with 2 steps in flight and an online softmax (MFMA QK^T and PV), and
-//      the waves combine in LDS.  The parts'
-//      (m, l, o) partials go out with agent-scope stores; the block that
-//      completes a (request, KV head) count merges them into the output.
-// The counters return to zero before each launch ends, so the next call (or a
+//      the waves combine in LDS.  The parts' (m, l, o) partials go out with
+//      agent-scope stores; the block that completes a (request, KV head)
+//      count merges them into the output.
+// The counters return to zero before the launch ends, so the next call (or a
 // graph replay) starts clean.  A CU streams only ~30-40 GB/s of these 256-byte
 // row slices, so the attention grid covers every CU.
 //
@@ -33,8 +32,6 @@ namespace qq {
 namespace {
 
 constexpr int kStepKV = 4;            // KV heads of the fused path (KV*D = 512)
-constexpr int kStepM = 8;             // bounds words per lane (512 / 64)
-constexpr int kStepPagesPerTile = 32; // score tile: 4 waves x 8 pages
 constexpr int kStepMaxG = 16;
 constexpr int kMaxSelFused = 64;
 constexpr int kStepMaxTopK = 4096;
@@ -51,97 +48,20 @@ struct StepArgs {
   int64_t r2t_stride, r2t_rows;
   float sl2;               // scale * log2(e)
   uint16_t* out;           // [bs, H * 128] bf16
-  int32_t* pages;          // [bs, 64] selected pages by rank (workspace)
   float* part_o;           // [bs, KV, parts, G, 128] attention partials (workspace)
   float* part_ml;          // [bs, KV, parts, G, 2] (m in log2 units, l)
   uint32_t* sync;
-  int bs, tiles_s, G;
+  int bs, G;
   int parts, per_wave;     // attention blocks per (request, KV head); rows per wave
   const int64_t* rows_in;  // rows given [bs, rows_stride] (attention over given rows)
   int64_t rows_stride;
   const int32_t* actual;   // [bs] attended slots (attention over given rows)
 };
 
-// sync (uint32 words, each counter on its own 128-byte line): score count [bs],
-// attention count [bs * KV].
-__device__ inline uint32_t* score_count(const StepArgs& a, int b) { return a.sync + b * 32; }
-__device__ inline uint32_t* attn_count(const StepArgs& a, int bh) { return a.sync + (a.bs + bh) * 32; }
+// sync: one counter per (request, KV head), each on its own 128-byte line.
+__device__ inline uint32_t* attn_count(const StepArgs& a, int bh) { return a.sync + bh * 32; }
 
 __device__ inline bool needs_selection(const SelectArgs& sa, int64_t s) { return s > sa.top_k && sa.k_sel > 0; }
-
-template <int KPT>
-union ScoreSmem {
-  float q[kMaxC];
-  SelectSmem<KPT> sel;
-};
-
-// The request's selection (quest.py:409-464), run by the block that completed
-// its score count: the top-k pages by rank into the page list, and the new
-// token's K/V (C = 512 bf16 = 256 words per row).
-template <int KPT>
-__device__ void select_request(const StepArgs& a, int b, ScoreSmem<KPT>& sm) {
-  const SelectArgs& sa = a.s;
-  const int tid = threadIdx.x;
-  const int64_t s = sa.seq[b];
-  const int64_t req = sa.rpi[b];
-  const int lim = (req >= 0 && req < sa.R) ? min(sa.limit[b], sa.MP) : 0;
-  const int k = sa.k_sel;
-  const int64_t loc = sa.new_k ? sa.new_locs[b] : -1;
-  uint32_t kw = 0u, vw = 0u;
-  if (sa.new_k) {
-    kw = static_cast<const uint32_t*>(sa.new_k)[(int64_t)b * 256 + tid];
-    vw = static_cast<const uint32_t*>(sa.new_v)[(int64_t)b * 256 + tid];
-  }
-  if (needs_selection(sa, s)) {
-    const float* sc = sa.scores + (int64_t)b * sa.MP;
-    float sv[KPT];
-#pragma unroll
-    for (int i = 0; i < KPT; ++i) {
-      const int p = tid + kBlock * i;
-      sv[i] = p < lim ? ld_agent(sc + p) : 0.0f;
-    }
-    select_topk_block<KPT>(sv, lim, max(lim, k), k, sm.sel);
-    if (tid < k) a.pages[b * kMaxSelFused + tid] = sm.sel.order[tid];
-  }
-  if (loc >= 0 && loc < sa.pool_rows) {
-    static_cast<uint32_t*>(sa.k_pool)[loc * 256 + tid] = kw;
-    static_cast<uint32_t*>(sa.v_pool)[loc * 256 + tid] = vw;
-  }
-}
-
-template <int KPT>
-__global__ __launch_bounds__(kBlock) void quest_score_select_kernel(StepArgs a) {
-  __shared__ ScoreSmem<KPT> sm;
-  __shared__ uint32_t s_last;
-  const SelectArgs& sa = a.s;
-  const int tid = threadIdx.x;
-  const int b = blockIdx.x / a.tiles_s, t = blockIdx.x - b * a.tiles_s;
-  const int64_t s = sa.seq[b];
-  const int64_t req = sa.rpi[b];
-  const int lim = (req >= 0 && req < sa.R) ? min(sa.limit[b], sa.MP) : 0;
-  const int p0 = t * kStepPagesPerTile;
-  if (needs_selection(sa, s) && p0 < lim) {  // block-uniform
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int lane = tid & 63;
-    const int pw = p0 + wave * 8;
-    uint32_t w[8][kStepM];
-    load_8pages<kStepM>(w, sa.bounds_layer + req * sa.MP * (64 * kStepM), pw, lim, lane);
-    block_qbar(sm.q, sa, b);
-    __syncthreads();
-    if (pw < lim) {
-      const float v = score_8pages<kStepM>(w, sm.q, lane);
-      const int p = pw + (lane >> 3);
-      if ((lane & 7) == 0 && p < lim) st_agent(sa.scores + (int64_t)b * sa.MP + p, v);
-    }
-  }
-  wait_memory();
-  __syncthreads();
-  if (tid == 0) s_last = add_agent(score_count(a, b), 1u) == (uint32_t)(a.tiles_s - 1);
-  __syncthreads();
-  if (!s_last) return;
-  if (tid == 0) st_agent(score_count(a, b), 0u);
-  select_request<KPT>(a, b, sm);
-}
 
 // One wave's step: the K and V slices of 32 layout rows of one KV head
 // (lane layouts of attn_wave64: K tile t = tokens 16t .. 16t+15, V k-step u =
@@ -244,12 +164,17 @@ struct HeadSmem {
 // stores an (m, l, o) partial (agent scope) and the block that completes the
 // (request, KV head) count merges the parts.  ROWS: the pool rows of the slots
 // are given (rows_in, actual) instead of coming from the page list and
-// req_to_token - the same arithmetic over the same slot order.
-template <bool ROWS>
+// req_to_token - the same arithmetic over the same slot order.  Otherwise the
+// block first selects its request's pages itself (quest.py:450-452) from the
+// scores of the scoring launch - every block of the request computes the same
+// list - with a KPT x 512-page selection that aliases the LDS the row table
+// and the wave combine use later.
+template <bool ROWS, int KPT>
 __global__ __launch_bounds__(64 * kHeadWaves, 1) void quest_attend_part_kernel(StepArgs a) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   HeadSmem& sm = *reinterpret_cast<HeadSmem*>(smem_raw);
   __shared__ uint32_t s_last;
+  __shared__ int32_t s_pages[kMaxSelFused];
   const SelectArgs& sa = a.s;
   constexpr int kThreads = 64 * kHeadWaves;
   const int tid = threadIdx.x;
@@ -271,6 +196,22 @@ __global__ __launch_bounds__(64 * kHeadWaves, 1) void quest_attend_part_kernel(S
   const int per_wave = a.per_wave;
   const int per_block = kHeadWaves * per_wave;  // <= kStepMaxTopK
   const int slot_base = part * per_block;
+  if (!ROWS && long_b && slot_base < k * P) {  // block-uniform: this block attends selected pages
+    static_assert(ROWS || KPT > 0, "selection capacity");
+    constexpr int kSel = KPT > 0 ? KPT : 1;
+    SelectSmem<kSel, kThreads>& ss = *reinterpret_cast<SelectSmem<kSel, kThreads>*>(smem_raw);
+    const int lim = (req >= 0 && req < sa.R) ? min(sa.limit[b], sa.MP) : 0;
+    const float* sc = sa.scores + (int64_t)b * sa.MP;
+    float sv[kSel];
+#pragma unroll
+    for (int i = 0; i < kSel; ++i) {
+      const int p = tid + kThreads * i;
+      sv[i] = p < lim ? sc[p] : 0.0f;
+    }
+    select_topk_block<kSel, kThreads>(sv, lim, max(lim, k), k, ss);
+    if (tid < k) s_pages[tid] = ss.order[tid];
+    __syncthreads();  // the list is in s_pages before the row table reuses the LDS
+  }
   int32_t* pos_out = !ROWS && h == 0 ? sa.positions + (int64_t)b * top_k : nullptr;
   for (int i0 = 0; i0 < per_block; i0 += kThreads * 4) {
     int64_t pv[4];
@@ -287,7 +228,7 @@ __global__ __launch_bounds__(64 * kHeadWaves, 1) void quest_attend_part_kernel(S
       if (!long_b)
         p = s <= top_k ? min((int64_t)slot, max(s - 1, (int64_t)0)) : min(max(s - P, (int64_t)0) + slot, s - 1);
       else if (slot < k * P)
-        p = (int64_t)a.pages[b * kMaxSelFused + slot / P] * P + slot % P;
+        p = (int64_t)s_pages[slot / P] * P + slot % P;
       else
         p = min(max(s - P, (int64_t)0) + (slot - k * P), s - 1);
       pv[u] = p;
@@ -439,7 +380,7 @@ using namespace qq;
 
 extern "C" int64_t qq_quest_layer_step_sync_bytes(int bs, int kv_heads) {
   if (bs <= 0 || kv_heads <= 0) return 0;
-  return (int64_t)bs * (1 + kv_heads) * 32 * (int64_t)sizeof(uint32_t);
+  return (int64_t)bs * kv_heads * 32 * (int64_t)sizeof(uint32_t);
 }
 
 // Compute units of the current device (cached per device).
@@ -455,18 +396,24 @@ static int device_cu_count() {
   return cached[dev];
 }
 
-// LDS of the attention kernels (above the 64 KiB default: opted in once per device).
+// LDS of an attention kernel instance (above the 64 KiB default: opted in once
+// per device).
+template <bool ROWS, int KPT>
 static size_t head_smem_bytes() {
+  static_assert(sizeof(SelectSmem<(KPT > 0 ? KPT : 1), 64 * kHeadWaves>) <= sizeof(HeadSmem), "aliased LDS");
   static bool opted[64] = {false};
   int dev = 0;
   if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64 && !opted[dev]) {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&quest_attend_part_kernel<false>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)sizeof(HeadSmem));
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&quest_attend_part_kernel<true>),
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&quest_attend_part_kernel<ROWS, KPT>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)sizeof(HeadSmem));
     opted[dev] = true;
   }
   return sizeof(HeadSmem);
+}
+
+template <int KPT>
+static void launch_attend_select(const StepArgs& a, int blocks, hipStream_t s) {
+  quest_attend_part_kernel<false, KPT><<<blocks, 64 * kHeadWaves, head_smem_bytes<false, KPT>(), s>>>(a);
 }
 
 // Shapes the fused layer step takes (bf16, KV*D = 4*128, G <= 16, page 64, at
@@ -531,7 +478,7 @@ int qq::attend_rows_fused(const void* q, int64_t q_bstride, int num_q_heads, con
   a.rows_in = rows;
   a.rows_stride = slots;
   a.actual = actual;
-  quest_attend_part_kernel<true><<<bs * kStepKV * parts, 64 * kHeadWaves, head_smem_bytes(), s>>>(a);
+  quest_attend_part_kernel<true, 0><<<bs * kStepKV * parts, 64 * kHeadWaves, head_smem_bytes<true, 0>(), s>>>(a);
   return QQ_OK;
 }
 
@@ -594,16 +541,21 @@ static int forward_decode(
   sa.pool_rows = kv_rows;
 
   const int G = num_q_heads / kv_heads;
-  const int64_t pages_bytes = (int64_t)bs * kMaxSelFused * (int64_t)sizeof(int32_t);
   const int parts = step_parts(bs, kv_heads, top_k);
   const int per_wave = ceil_div(top_k, parts * kHeadWaves * 32) * 32;
   const int64_t part_bytes = (int64_t)bs * kv_heads * parts * G * (kMfmaDim + 2) * (int64_t)sizeof(float);
   const bool fused = sync && sync_bytes >= qq_quest_layer_step_sync_bytes(bs, kv_heads) &&
                      fused_shape(q_dtype, kv_dtype, k_new ? new_dtype : -1, num_q_heads, kv_heads, head_dim,
                                  page_size, top_k, max_pages) &&
-                     workspace && workspace_bytes >= pages_bytes + (parts > 1 ? part_bytes : 0);
+                     workspace && workspace_bytes >= (parts > 1 ? part_bytes : 0);
   if (fused) {
-    StepArgs a;
+    // 1. scores of the candidate pages (+ the new token's K/V), all CUs
+    if (phase & 1) {
+      const int st = launch_score(sa, bs, true, s);
+      if (st != QQ_OK || !(phase & 2)) return st;
+    }
+    // 2. per (request, KV head, part): the request's selection, layout, attention, merge
+    StepArgs a{};
     a.s = sa;
     a.k = static_cast<const uint16_t*>(k_layer);
     a.v = static_cast<const uint16_t*>(v_layer);
@@ -613,31 +565,26 @@ static int forward_decode(
     a.r2t_rows = req_to_token_rows;
     a.sl2 = scale * kLog2e;
     a.out = static_cast<uint16_t*>(out);
-    a.pages = static_cast<int32_t*>(workspace);
-    a.part_o = reinterpret_cast<float*>(static_cast<char*>(workspace) + pages_bytes);
+    a.part_o = static_cast<float*>(workspace);
     a.part_ml = a.part_o + (int64_t)bs * kv_heads * parts * G * kMfmaDim;
     a.parts = parts;
     a.per_wave = per_wave;
     a.sync = static_cast<uint32_t*>(sync);
     a.bs = bs;
-    a.tiles_s = ceil_div(max(max_pages, 1), kStepPagesPerTile);
     a.G = G;
-    const int score_blocks = bs * a.tiles_s;
+    const int blocks = bs * kStepKV * parts;
+    constexpr int kT = 64 * kHeadWaves;
     const int n_max = max(max_pages, k_sel);
-    if (!(phase & 1))
-      ;
-    else if (n_max <= 4 * kBlock)
-      quest_score_select_kernel<4><<<score_blocks, kBlock, 0, s>>>(a);
-    else if (n_max <= 8 * kBlock)
-      quest_score_select_kernel<8><<<score_blocks, kBlock, 0, s>>>(a);
-    else if (n_max <= 12 * kBlock)
-      quest_score_select_kernel<12><<<score_blocks, kBlock, 0, s>>>(a);
-    else if (n_max <= 16 * kBlock)
-      quest_score_select_kernel<16><<<score_blocks, kBlock, 0, s>>>(a);
+    if (n_max <= 2 * kT)
+      launch_attend_select<2>(a, blocks, s);
+    else if (n_max <= 4 * kT)
+      launch_attend_select<4>(a, blocks, s);
+    else if (n_max <= 6 * kT)
+      launch_attend_select<6>(a, blocks, s);
+    else if (n_max <= 8 * kT)
+      launch_attend_select<8>(a, blocks, s);
     else
-      quest_score_select_kernel<24><<<score_blocks, kBlock, 0, s>>>(a);
-    if (phase & 2)
-      quest_attend_part_kernel<false><<<bs * kStepKV * parts, 64 * kHeadWaves, head_smem_bytes(), s>>>(a);
+      launch_attend_select<12>(a, blocks, s);
     return check_launch(what);
   }
 

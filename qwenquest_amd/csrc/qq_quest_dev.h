@@ -233,59 +233,63 @@ __device__ inline float score_8pages(const uint32_t (&w)[8][M], const float* s_q
 
 constexpr uint32_t kNegInfKey = 0x007FFFFFu;  // orderable(-inf): masked pages (quest.py:451)
 
-template <int KPT>
+template <int KPT, int NT = kBlock>
 struct SelectSmem {
-  uint64_t cand[kBlock * KPT + 64];  // survivors, flattened (zero-padded up to 64)
-  uint64_t gmax[64];                 // maxima of the 64 groups of 4 threads
-  int grank[64];                     // number of group maxima above each group's
-  int crank[64];                     // number of survivors above each survivor (<= 64 of them)
-  int wcnt[kBlockWaves];
+  uint64_t cand[NT * KPT + 64];  // survivors, flattened (zero-padded up to 64)
+  uint64_t gmax[64];             // maxima of the 64 groups of NT/64 threads
+  int grank[64];                 // number of group maxima above each group's
+  int crank[64];                 // number of survivors above each survivor (<= 64 of them)
+  int wcnt[NT / 64];
   uint64_t tau;
   int order[64];
 };
 
-// Top k <= 64 pages of n_eff <= 256*KPT keys (quest.py:450-452), whole block:
-// sv[i] is the score of page tid + 256 i (pages >= lim rank as -inf).  Keys
-// are (order-preserving score, ~page), so "larger" = higher score, then lower
-// page, and all keys differ.
-//   1. tau = the k-th largest of the maxima of 64 groups of 4 threads (1 when
-//      fewer than k groups hold keys).  The k largest group maxima are k
+// Top k <= 64 pages of n_eff <= NT*KPT keys (quest.py:450-452), whole block of
+// NT threads: sv[i] is the score of page tid + NT i (pages >= lim rank as
+// -inf).  Keys are (order-preserving score, ~page), so "larger" = higher
+// score, then lower page, and all keys differ.
+//   1. tau = the k-th largest of the maxima of 64 groups of NT/64 threads (1
+//      when fewer than k groups hold keys).  The k largest group maxima are k
 //      distinct keys >= tau, so every top-k key is >= tau;
 //   2. the keys >= tau (at least k; about 40 of 2048 for distinct scores) are
 //      compacted into one LDS array (ballot + mbcnt within a wave, wave counts
 //      give the offsets);
-//   3. each survivor's rank = number of survivors above it (split over the 4
+//   3. each survivor's rank = number of survivors above it (split over the
 //      waves when there are at most 64); ranks < k give the pages in
 //      (score desc, page asc) order in s.order[0, k).
-template <int KPT>
-__device__ inline void select_topk_block(const float (&sv)[KPT], int lim, int n_eff, int k, SelectSmem<KPT>& s) {
+template <int KPT, int NT = kBlock>
+__device__ inline void select_topk_block(const float (&sv)[KPT], int lim, int n_eff, int k,
+                                         SelectSmem<KPT, NT>& s) {
+  static_assert(NT == 256 || NT == 512, "64 groups of whole quads or octets");
+  constexpr int NW = NT / 64, GS = NT / 64, SHARE = 64 / NW;
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   uint64_t key[KPT];
   uint64_t tmax = 0ull;
 #pragma unroll
   for (int i = 0; i < KPT; ++i) {
-    const int p = tid + kBlock * i;
+    const int p = tid + NT * i;
     key[i] = p < n_eff ? sel_key(p < lim ? orderable(sv[i]) : kNegInfKey, p) : 0ull;
     tmax = key[i] > tmax ? key[i] : tmax;
   }
   uint64_t g = tmax;
-  uint64_t o = __shfl_xor(g, 1, 64);
-  g = o > g ? o : g;
-  o = __shfl_xor(g, 2, 64);
-  g = o > g ? o : g;
-  if ((tid & 3) == 0) s.gmax[tid >> 2] = g;
+#pragma unroll
+  for (int m = 1; m < GS; m <<= 1) {
+    const uint64_t o = __shfl_xor(g, m, 64);
+    g = o > g ? o : g;
+  }
+  if (tid % GS == 0) s.gmax[tid / GS] = g;
   if (tid < 64) {
     s.grank[tid] = 0;
     s.crank[tid] = 0;
   }
   if (tid == 0) s.tau = 1ull;
   __syncthreads();
-  // group i's rank, a quarter of the comparisons per wave
+  // group i's rank, 1/NW of the comparisons per wave
   const uint64_t gi = s.gmax[lane];
   int part = 0;
 #pragma unroll
-  for (int j = 0; j < 16; ++j) part += s.gmax[wave * 16 + j] > gi;
+  for (int j = 0; j < SHARE; ++j) part += s.gmax[wave * SHARE + j] > gi;
   atomicAdd(&s.grank[lane], part);
   __syncthreads();
   if (tid < 64 && gi != 0ull && s.grank[tid] == k - 1) s.tau = gi;  // unique: nonzero keys differ
@@ -302,7 +306,7 @@ __device__ inline void select_topk_block(const float (&sv)[KPT], int lim, int n_
   __syncthreads();
   int base = 0, total = 0;
 #pragma unroll
-  for (int w = 0; w < kBlockWaves; ++w) {
+  for (int w = 0; w < NW; ++w) {
     const int c = s.wcnt[w];
     base += w < wave ? c : 0;
     total += c;
@@ -317,11 +321,11 @@ __device__ inline void select_topk_block(const float (&sv)[KPT], int lim, int n_
   if (tid >= total && tid < 64) s.cand[tid] = 0ull;  // a zero key ranks above nothing
   __syncthreads();
   if (total <= 64) {
-    // survivor `lane`'s rank, a quarter of the comparisons per wave
+    // survivor `lane`'s rank, 1/NW of the comparisons per wave
     const uint64_t ci = s.cand[lane];
     int part = 0;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) part += s.cand[wave * 16 + j] > ci;
+    for (int j = 0; j < SHARE; ++j) part += s.cand[wave * SHARE + j] > ci;
     atomicAdd(&s.crank[lane], part);
     __syncthreads();
     if (tid < total) {
@@ -329,7 +333,7 @@ __device__ inline void select_topk_block(const float (&sv)[KPT], int lim, int n_
       if (r < k) s.order[r] = (int)(~(uint32_t)s.cand[tid]);
     }
   } else {
-    for (int i = tid; i < total; i += kBlock) {
+    for (int i = tid; i < total; i += NT) {
       const uint64_t ci = s.cand[i];
       int r = 0;
       for (int j = 0; j < total; ++j) r += s.cand[j] > ci;

@@ -90,8 +90,7 @@ def test_library_has_no_host_fallback_symbols(lib):
 
 def test_forward_decode_phase_is_validated_without_gpu(lib):
     """A phase other than 1, 2 or 3 is refused (QQ_EINVAL) before any HIP call; the
-    fused layer step's sync buffer holds one 128-byte counter line per request and one
-    per (request, KV head)."""
+    fused layer step's sync buffer holds one 128-byte counter line per (request, KV head)."""
     from qwenquest_amd import _lib
 
     fake = ctypes.c_void_p(16)  # never dereferenced: validation fails first
@@ -100,7 +99,7 @@ def test_forward_decode_phase_is_validated_without_gpu(lib):
     for phase in (0, 4, -1):
         st = lib.qq_quest_forward_decode_phase(*args, phase, None)
         assert st == _lib.QQ_EINVAL and b"phase" in lib.qq_last_error()
-    assert lib.qq_quest_layer_step_sync_bytes(16, 4) == 16 * (1 + 4) * 128
+    assert lib.qq_quest_layer_step_sync_bytes(16, 4) == 16 * 4 * 128
     assert lib.qq_quest_layer_step_sync_bytes(0, 4) == 0
 
 
