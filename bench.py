@@ -8,7 +8,7 @@ synthetic N(0, 1) from fixed seeds.
 
 One step = one decode step of all 48 layers through the drop-in backend:
 bounds append (fused over layers) + per layer two launches: GQA-mean page
-scoring + per-request top-31 selection + new K/V write, then layout,
+scoring + new K/V write, then per-request top-31 selection, layout,
 req_to_token gather and attention.  The step is captured once in a HIP graph
 and replayed; seq_lens advance by one token per replay, so pages complete and
 get finalized during the run.  Reported value: microseconds per layer-step
@@ -344,7 +344,7 @@ def main() -> int:
     byts = algorithmic_bytes(seqs_timed, P, TOP_K, 2 * KV * D * 2, KV * D * 2 * 2)
     step_frac = byts["headline"] / (us_per_layer_step * 1e-6) / (HBM_PEAK_GBS * 1e9)
 
-    # per-kernel durations of the layer step's two launches (score + select, attention),
+    # per-kernel durations of the layer step's two launches (scores, selection + attention),
     # each from a graph of L launches over the L layers in turn (so that no launch finds its
     # bounds or K/V rows in a cache, as in the step), HIP events on the launch stream
     torch.add(base, seq_lens - 1, out=out_loc)

@@ -219,9 +219,10 @@ __global__ __launch_bounds__(64 * kHeadWaves, 1) void quest_attend_part_kernel(S
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int slot = slot_base + i0 + tid + kThreads * u;
+      const bool mine = i0 + tid + kThreads * u < per_block;  // only this block's share is read
       if (ROWS) {
         pv[u] = 0;
-        rv[u] = slot < n ? a.rows_in[(int64_t)b * a.rows_stride + slot] : 0;
+        rv[u] = mine && slot < n ? a.rows_in[(int64_t)b * a.rows_stride + slot] : 0;
         continue;
       }
       int64_t p;
@@ -232,7 +233,7 @@ __global__ __launch_bounds__(64 * kHeadWaves, 1) void quest_attend_part_kernel(S
       else
         p = min(max(s - P, (int64_t)0) + (slot - k * P), s - 1);
       pv[u] = p;
-      rv[u] = (slot < n && r2t_ok && p >= 0 && p < a.r2t_stride) ? a.r2t[req * a.r2t_stride + p] : 0;
+      rv[u] = (mine && slot < n && r2t_ok && p >= 0 && p < a.r2t_stride) ? a.r2t[req * a.r2t_stride + p] : 0;
     }
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
