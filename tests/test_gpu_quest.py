@@ -522,6 +522,83 @@ def test_forward_decode_fused_path_engine_flow(flow):
         assert not step_counters(be, len(reqs)).any()  # the fused path leaves its counters at zero
 
 
+R2T_LAYOUTS = ("page_runs", "scattered", "mixed")
+
+
+@pytest.mark.parametrize("layout", R2T_LAYOUTS)
+def test_fused_step_req_to_token_layouts(layout):
+    """The fused layer step over req_to_token layouts that are not one run per request:
+    pages as runs at shuffled bases, scattered rows, and page runs broken by swapped rows.
+    Positions bit-exact vs the oracle, outputs within 2e-2 of the oracle's attention over
+    r2t[req, positions]."""
+    from qwenquest_amd.attention.quest_only import QuestOnlyBackend
+    from qwenquest_amd.batch import ForwardBatch, ForwardMode
+    from qwenquest_amd.memory import MHATokenToKVPool, ReqToTokenPool
+
+    H, KV, D, P, TOP_K, CTX = 32, 4, 128, 64, 1024, 3200
+    prompt = {0: 3000, 1: 1500, 2: 2100}
+    steps = 4
+    nreq = len(prompt)
+    rows_total = nreq * CTX + 1
+    gen = np.random.default_rng(R2T_LAYOUTS.index(layout) + 11)
+    if layout == "scattered":
+        r2t = (gen.permutation(nreq * CTX) + 1).astype(np.int32).reshape(nreq, CTX)
+    else:
+        bases = gen.permutation(nreq * CTX // P)[: nreq * (CTX // P)] * P + 1
+        r2t = (bases[:, None] + np.arange(P)[None]).reshape(nreq, CTX).astype(np.int32)
+        if layout == "mixed":
+            for r in range(nreq):
+                for pg in range(r, CTX // P, 3):  # every third page: two rows swapped
+                    a, b = pg * P + 5, pg * P + 40
+                    r2t[r, a], r2t[r, b] = r2t[r, b], r2t[r, a]
+    rtp = ReqToTokenPool(nreq, CTX, DEV)
+    rtp.req_to_token.copy_(torch.from_numpy(r2t).to(DEV))
+    kvp = MHATokenToKVPool(rows_total - 1, 1, KV, D, torch.bfloat16, DEV)
+    be = QuestOnlyBackend(rtp, kvp, {"algorithm": "quest", "top_k": TOP_K, "quest_page_size": P})
+    st = oq.QuestState(TOP_K, P)
+    st.init_storage(0, 1, nreq, CTX, KV, D)
+    kk = rand_bf16((1, rows_total, KV, D), seed=81)
+    vv = rand_bf16((1, rows_total, KV, D), seed=82)
+    kb, vb = bf16.to_f32(bf16_bits(kk)), bf16.to_f32(bf16_bits(vv))
+    for r, n in prompt.items():
+        rows = torch.from_numpy(r2t[r, :n].astype(np.int64))
+        kvp.k_all[:, rows] = kk[:, rows].to(DEV)
+        kvp.v_all[:, rows] = vv[:, rows].to(DEV)
+        be.quest.update_prefill_representations_fused(r, kvp.k_all, rtp.req_to_token[r, :n])
+        be._skip_first_decode_update[r] = True
+        st.update_prefill_representations(0, r, bf16_bits(kk[0]), rows.numpy())
+    reqs = sorted(prompt)
+
+    class Layer:
+        layer_id, scaling = 0, D**-0.5
+
+    for step in range(steps):
+        seqs = [prompt[r] + step + 1 for r in reqs]
+        locs = torch.tensor([int(r2t[r, s - 1]) for r, s in zip(reqs, seqs)], device=DEV)
+        batch = ForwardBatch(ForwardMode.DECODE, None, None, torch.tensor(reqs, device=DEV),
+                             torch.tensor(seqs, device=DEV), locs, rtp, kvp, be)
+        be.init_forward_metadata(batch)
+        if step > 0:
+            prev = np.array([r2t[r, s - 2] for r, s in zip(reqs, seqs)])
+            st.update_decode_representations(0, reqs, bf16_bits(kk[0]), prev)
+            st.maybe_finalize_decode_representations(reqs)
+        st.prepare_step(seqs)
+        q = rand_bf16((len(reqs), H, D), seed=400 + step)
+        lc = locs.cpu()
+        out = be.forward_decode(q.to(DEV), kk[0, lc].to(DEV), vv[0, lc].to(DEV), Layer(), batch)
+        pos = be._positions[: len(reqs)].clone()
+        ref_pos, ref_actual, _ = st.retrieve_topk(q.float().numpy(), 0, reqs)
+        got_pos = pos.cpu().numpy()
+        rows = []
+        for i, r in enumerate(reqs):
+            n = int(ref_actual[i])
+            assert np.array_equal(got_pos[i, :n], ref_pos[i, :n]), f"step {step} r{r}"
+            rows.append(r2t[r, ref_pos[i, :n]].astype(np.int64))
+        ref = oa.sparse_decode(q.float().numpy(), kb[0], vb[0], rows, D**-0.5)
+        assert np.abs(out.float().cpu().numpy() - ref).max() < 2e-2
+    assert not step_counters(be, len(reqs)).any()
+
+
 def test_positions_and_rows_entries_are_bit_identical():
     """qq_quest_decode_attention (positions through req_to_token) and
     qq_decode_attention_rows (rows given) on the same rows give the same bits, with
