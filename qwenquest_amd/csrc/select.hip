@@ -145,6 +145,10 @@ __global__ __launch_bounds__(kThreads) void score_candidates_kernel(SelectArgs a
 // operations in the same order as lane_partial.  Pages past the candidate limit
 // re-read the limit's last page and are not stored, so every load is issued
 // unconditionally.
+//
+// Tile 0 of a request also stores the new token's K/V (set_kv_buffer); its
+// loads go out with the page loads and its stores after the scores, so that
+// the block's pages are not held back by the copy's round trips.
 template <int M>
 __global__ __launch_bounds__(kThreads) void score_pages_fast_kernel(SelectArgs a, int store_new) {
   constexpr int C = 64 * M;
@@ -152,9 +156,22 @@ __global__ __launch_bounds__(kThreads) void score_pages_fast_kernel(SelectArgs a
   const int64_t s = a.seq[b];
   const int lim = min(a.limit[b], a.MP);
   const int64_t req = a.rpi[b];
-  if (store_new && blockIdx.x == 0) store_new_token(a, b);
   const int p0 = blockIdx.x * a.ppb;
-  if (s <= a.top_k || a.k_sel == 0 || p0 >= lim || req < 0 || req >= a.R) return;
+  const bool copy_new = store_new && blockIdx.x == 0;
+  if (s <= a.top_k || a.k_sel == 0 || p0 >= lim || req < 0 || req >= a.R) {
+    if (copy_new) store_new_token(a, b);
+    return;
+  }
+  // the new token as 16-byte pieces of bf16 rows of C elements, one per thread
+  static_assert(C / 8 <= kThreads, "one 16-byte piece of K and of V per thread");
+  const bool copy_fast = copy_new && a.new_k && a.new_dtype == QQ_DTYPE_BF16 && a.pool_dtype == QQ_DTYPE_BF16;
+  uint4 nk = make_uint4(0u, 0u, 0u, 0u), nv = nk;
+  int64_t loc = -1;
+  if (copy_fast && threadIdx.x < C / 8) {
+    loc = a.new_locs[b];
+    nk = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.new_k) + (int64_t)b * C)[threadIdx.x];
+    nv = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.new_v) + (int64_t)b * C)[threadIdx.x];
+  }
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int pw = p0 + wave * 8;  // this wave's 8 pages
@@ -163,10 +180,19 @@ __global__ __launch_bounds__(kThreads) void score_pages_fast_kernel(SelectArgs a
   __shared__ float s_q[kMaxC];
   block_qbar(s_q, a, b);
   __syncthreads();
-  if (pw >= lim) return;
-  const float v = score_8pages<M>(w, s_q, lane);
-  const int p = pw + (lane >> 3);
-  if ((lane & 7) == 0 && p < lim) a.scores[(int64_t)b * a.MP + p] = v;
+  if (pw < lim) {
+    const float v = score_8pages<M>(w, s_q, lane);
+    const int p = pw + (lane >> 3);
+    if ((lane & 7) == 0 && p < lim) a.scores[(int64_t)b * a.MP + p] = v;
+  }
+  if (copy_fast) {
+    if (threadIdx.x < C / 8 && loc >= 0 && loc < a.pool_rows) {
+      reinterpret_cast<uint4*>(static_cast<uint16_t*>(a.k_pool) + loc * C)[threadIdx.x] = nk;
+      reinterpret_cast<uint4*>(static_cast<uint16_t*>(a.v_pool) + loc * C)[threadIdx.x] = nv;
+    }
+  } else if (copy_new) {
+    store_new_token(a, b);
+  }
 }
 
 // One block per request: top k_sel pages (quest.py:450-452) + token layout (453-460).
