@@ -172,14 +172,55 @@ __global__ __launch_bounds__(kThreads) void score_pages_fast_kernel(SelectArgs a
     nk = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.new_k) + (int64_t)b * C)[threadIdx.x];
     nv = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.new_v) + (int64_t)b * C)[threadIdx.x];
   }
+  // bf16 queries with G <= 8: the request's query words are loaded before the
+  // pages and q-bar is computed while the pages are in flight (the same fp32
+  // operations in the same order as block_qbar); other queries after them
+  const int G = a.H / a.KV;
+  const bool q_early = a.q_dtype == QQ_DTYPE_BF16 && a.D % 2 == 0 && G > 1 && G <= 8;
+  constexpr int kPairs = (C / 2 + kThreads - 1) / kThreads;  // channel pairs per thread
+  uint32_t qw[kPairs][8];
+  if (q_early) {
+#pragma unroll
+    for (int j = 0; j < kPairs; ++j) {
+      const int c = (threadIdx.x + kThreads * j) * 2;
+      if (c < C) {
+        const int h = c / a.D, d = c - h * a.D;
+        const uint32_t* qp = reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(a.q) +
+                                                               (int64_t)b * a.q_bstride + (int64_t)h * G * a.D + d);
+#pragma unroll
+        for (int g = 0; g < 8; ++g) qw[j][g] = g < G ? qp[(int64_t)g * (a.D / 2)] : 0u;
+      }
+    }
+    __asm__ volatile("" ::: "memory");  // the query loads go out before the page loads
+  }
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int pw = p0 + wave * 8;  // this wave's 8 pages
   uint32_t w[8][M];
   load_8pages<M>(w, a.bounds_layer + req * a.MP * C, pw, lim, lane);
   __shared__ float s_q[kMaxC];
-  block_qbar(s_q, a, b);
-  __syncthreads();
+  if (q_early) {
+#pragma unroll
+    for (int j = 0; j < kPairs; ++j) {
+      const int c = (threadIdx.x + kThreads * j) * 2;
+      if (c < C) {
+        float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+        for (int g = 0; g < 8; ++g) {
+          if (g < G) {
+            a0 = __fadd_rn(a0, bf2f((uint16_t)(qw[j][g] & 0xFFFFu)));
+            a1 = __fadd_rn(a1, bf2f((uint16_t)(qw[j][g] >> 16)));
+          }
+        }
+        s_q[c] = bf2f(f2bf(a0 / (float)G));
+        s_q[c + 1] = bf2f(f2bf(a1 / (float)G));
+      }
+    }
+  } else {
+    block_qbar(s_q, a, b);
+  }
+  // LDS-only barrier: s_q is written; the page loads stay in flight
+  __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   if (pw < lim) {
     const float v = score_8pages<M>(w, s_q, lane);
     const int p = pw + (lane >> 3);
