@@ -261,7 +261,8 @@ __global__ __launch_bounds__(64 * kHeadWaves, 1) void quest_attend_part_kernel(S
       }
     }
   }
-  __syncthreads();
+  // the row table is in LDS; the position stores and query loads stay in flight
+  lds_barrier();
   // this wave's rows: local [r0, r0 + per_wave), real up to slot n
   const int r0 = wave * per_wave;
   const int r_end = max(r0, min(r0 + per_wave, n - slot_base));

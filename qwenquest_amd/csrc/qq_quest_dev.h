@@ -48,6 +48,11 @@ __device__ inline uint64_t ld_agent(const uint64_t* p) {
 // the memory clobber keeps the compiler from moving memory accesses across it.
 __device__ inline void wait_memory() { __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+// Block barrier for LDS hand-offs only: waits for this wave's LDS operations,
+// not for its global loads and stores (which __syncthreads waits for), so they
+// stay in flight across it; uses of their results get their own waits.
+__device__ inline void lds_barrier() { __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 // 16-byte agent-scope loads through a buffer resource (cache policy sc1, as
 // the agent-scope loads above use); offsets past `bytes` read zeros.
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));

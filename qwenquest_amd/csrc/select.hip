@@ -219,8 +219,7 @@ __global__ __launch_bounds__(kThreads) void score_pages_fast_kernel(SelectArgs a
   } else {
     block_qbar(s_q, a, b);
   }
-  // LDS-only barrier: s_q is written; the page loads stay in flight
-  __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  lds_barrier();  // s_q is written; the page loads stay in flight
   if (pw < lim) {
     const float v = score_8pages<M>(w, s_q, lane);
     const int p = pw + (lane >> 3);
