@@ -238,6 +238,18 @@ __device__ inline float score_8pages(const uint32_t (&w)[8][M], const float* s_q
 
 constexpr uint32_t kNegInfKey = 0x007FFFFFu;  // orderable(-inf): masked pages (quest.py:451)
 
+// DPP lane moves (data-parallel primitives, VALU only) of a 64-bit value, as two
+// 32-bit moves; every lane must be active.
+constexpr int kDppQuadXor1 = 0xB1;       // quad_perm [1, 0, 3, 2]
+constexpr int kDppQuadXor2 = 0x4E;       // quad_perm [2, 3, 0, 1]
+constexpr int kDppHalfRowMirror = 0x141; // lane i of each 8 -> lane 7 - i
+template <int CTRL>
+__device__ inline uint64_t dpp64(uint64_t v) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, CTRL, 0xF, 0xF, false);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(v >> 32), CTRL, 0xF, 0xF, false);
+  return ((uint64_t)hi << 32) | lo;
+}
+
 template <int KPT, int NT = kBlock>
 struct SelectSmem {
   uint64_t cand[NT * KPT + 64];  // survivors, flattened (zero-padded up to 64)
@@ -265,7 +277,7 @@ struct SelectSmem {
 template <int KPT, int NT = kBlock>
 __device__ inline void select_topk_block(const float (&sv)[KPT], int lim, int n_eff, int k,
                                          SelectSmem<KPT, NT>& s) {
-  static_assert(NT == 256 || NT == 512, "64 groups of whole quads or octets");
+  static_assert(NT == 256 || NT == 512, "64 groups of whole quads or octets");  // GS = 4 or 8
   constexpr int NW = NT / 64, GS = NT / 64, SHARE = 64 / NW;
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
@@ -277,10 +289,16 @@ __device__ inline void select_topk_block(const float (&sv)[KPT], int lim, int n_
     key[i] = p < n_eff ? sel_key(p < lim ? orderable(sv[i]) : kNegInfKey, p) : 0ull;
     tmax = key[i] > tmax ? key[i] : tmax;
   }
+  // group maximum over GS consecutive lanes with DPP moves (no LDS round trips):
+  // the other lane of each pair, the other pair of each quad, then (GS = 8)
+  // the other quad of each half row
   uint64_t g = tmax;
-#pragma unroll
-  for (int m = 1; m < GS; m <<= 1) {
-    const uint64_t o = __shfl_xor(g, m, 64);
+  uint64_t o = dpp64<kDppQuadXor1>(g);
+  g = o > g ? o : g;
+  o = dpp64<kDppQuadXor2>(g);
+  g = o > g ? o : g;
+  if (GS == 8) {
+    o = dpp64<kDppHalfRowMirror>(g);
     g = o > g ? o : g;
   }
   if (tid % GS == 0) s.gmax[tid / GS] = g;
