@@ -108,8 +108,9 @@ __device__ inline void attend_step(const StepRegs& r, const bf16x8_t (&qb)[4], i
       acc[t][i] = x;
       mx = fmaxf(mx, x);
     }
-  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  const int lane = threadIdx.x & 63;
+  mx = fmaxf(mx, lane_xor16(mx, lane));
+  mx = fmaxf(mx, lane_xor32(mx, lane));
   const float Mn = fmaxf(M, mx);
   const float alpha = M == -INFINITY ? 0.0f : exp2f(M - Mn);  // rescale of the running sums
   float sum = 0.0f;
@@ -122,8 +123,8 @@ __device__ inline void attend_step(const StepRegs& r, const bf16x8_t (&qb)[4], i
       sum += bf2f(pb);
       pa[t][i] = (short)pb;
     }
-  sum += __shfl_xor(sum, 16, 64);
-  sum += __shfl_xor(sum, 32, 64);
+  sum += lane_xor16(sum, lane);
+  sum += lane_xor32(sum, lane);
   L = L * alpha + sum;
   M = Mn;
   // o rows are heads 4hi + i: their scale factors live in lanes 4hi + i

@@ -155,6 +155,28 @@ __device__ inline void block_qbar(float* s_q, const SelectArgs& a, int b) {
   for (int c = threadIdx.x; c < a.C; c += kBlock) s_q[c] = gqa_mean(a.q, a.q_dtype, qb, G, a.D, c);
 }
 
+// Lane exchanges without the LDS: gfx950's permlane swaps across rows and DPP
+// moves within a row.  lane_xor32/16/8/2/1(v) = v of lane l ^ 32/16/8/2/1;
+// lane_up4(v) = v of lane l + 4 in the row, which is lane l ^ 4 for lanes with
+// bit 2 clear.  A permlane swap of (v, v) gives every lane the pair
+// {v of the lower row or half, v of the upper one}.
+__device__ inline float lane_xor32(float v, int lane) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float((lane & 32) ? r[0] : r[1]);
+}
+__device__ inline float lane_xor16(float v, int lane) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float((lane & 16) ? r[0] : r[1]);
+}
+template <int CTRL>
+__device__ inline float dpp_f32(float v) {
+  return __uint_as_float((uint32_t)__builtin_amdgcn_update_dpp(0, (int)__float_as_uint(v), CTRL, 0xF, 0xF, false));
+}
+__device__ inline float lane_xor8(float v) { return dpp_f32<0x128>(v); }  // row_ror:8
+__device__ inline float lane_up4(float v) { return dpp_f32<0x104>(v); }   // row_shl:4
+__device__ inline float lane_xor2(float v) { return dpp_f32<0x4E>(v); }   // quad_perm [2, 3, 0, 1]
+__device__ inline float lane_xor1(float v) { return dpp_f32<0xB1>(v); }   // quad_perm [1, 0, 3, 2]
+
 // Lane partials of 8 pages at once.  acc[p] is this lane's partial of page p
 // (its m channels, summed in order).  The 8 halving trees are interleaved: at
 // level w = 32, 16, 8 each lane keeps half of its pages and adds the partner's
@@ -167,24 +189,27 @@ __device__ inline float reduce8_pages(float (&acc)[8], int lane) {
   for (int j = 0; j < 4; ++j) {
     const float send = up32 ? acc[j] : acc[4 + j];
     const float keep = up32 ? acc[4 + j] : acc[j];
-    v4[j] = __fadd_rn(keep, __shfl_xor(send, 32, 64));
+    v4[j] = __fadd_rn(keep, lane_xor32(send, lane));
   }
   float v2[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const float send = up16 ? v4[j] : v4[2 + j];
     const float keep = up16 ? v4[2 + j] : v4[j];
-    v2[j] = __fadd_rn(keep, __shfl_xor(send, 16, 64));
+    v2[j] = __fadd_rn(keep, lane_xor16(send, lane));
   }
   float v;
   {
     const float send = up8 ? v2[0] : v2[1];
     const float keep = up8 ? v2[1] : v2[0];
-    v = __fadd_rn(keep, __shfl_xor(send, 8, 64));
+    v = __fadd_rn(keep, lane_xor8(send));
   }
-  v = __fadd_rn(v, __shfl_xor(v, 4, 64));
-  v = __fadd_rn(v, __shfl_xor(v, 2, 64));
-  v = __fadd_rn(v, __shfl_xor(v, 1, 64));
+  // levels 4, 2, 1: only lanes with bits 2..0 clear (one per page) return a
+  // result, and their chain reads lanes l ^ 4 with bit 2 clear, so lane l + 4
+  // stands in for l ^ 4
+  v = __fadd_rn(v, lane_up4(v));
+  v = __fadd_rn(v, lane_xor2(v));
+  v = __fadd_rn(v, lane_xor1(v));
   return v;
 }
 
@@ -443,8 +468,8 @@ __device__ inline void attn_wave64(const uint16_t* const* krow, const uint16_t* 
       acc[t][i] = x;
       mx = fmaxf(mx, x);
     }
-  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  mx = fmaxf(mx, lane_xor16(mx, l));
+  mx = fmaxf(mx, lane_xor32(mx, l));
   float sum = 0.0f;
   short4_t pa[4];
 #pragma unroll
@@ -455,8 +480,8 @@ __device__ inline void attn_wave64(const uint16_t* const* krow, const uint16_t* 
       sum += bf2f(pb);
       pa[t][i] = (short)pb;
     }
-  sum += __shfl_xor(sum, 16, 64);
-  sum += __shfl_xor(sum, 32, 64);
+  sum += lane_xor16(sum, l);
+  sum += lane_xor32(sum, l);
 
 #pragma unroll
   for (int e = 0; e < 8; ++e) o[e] = float4_t{0.f, 0.f, 0.f, 0.f};
