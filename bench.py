@@ -232,6 +232,84 @@ def hisparse_bench(args) -> int:
     return 0
 
 
+def dense_bench(args) -> int:
+    """Dense decode (every request attends its whole context, attention/dense.py:26-42) on the
+    same batch and contexts: the comparator the Quest layer step is measured against."""
+    from qwenquest_amd import _lib
+    from qwenquest_amd.attention.dense import DenseBackend
+    from qwenquest_amd.batch import ForwardBatch, ForwardMode
+    from qwenquest_amd.memory import MHATokenToKVPool, ReqToTokenPool
+
+    _lib.load()
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    B, S, L = args.batch, args.ctx, args.dense_layers
+    H, KV, D = 32, 4, 128
+    total_steps = args.warmup + args.steps + 2
+    span = S + total_steps + 64
+    max_ctx = span
+    rows = B * span
+    t_setup = time.perf_counter()
+    rtp = ReqToTokenPool(B, max_ctx, dev)
+    kvp = MHATokenToKVPool(rows, L, KV, D, torch.bfloat16, dev)
+    gen = torch.Generator(device=dev).manual_seed(1234)
+    for layer in range(L):
+        kvp.k_all[layer].normal_(generator=gen)
+        kvp.v_all[layer].normal_(generator=gen)
+    base = 1 + torch.arange(B, device=dev, dtype=torch.int64) * span
+    rtp.req_to_token.copy_((base[:, None] + torch.arange(max_ctx, device=dev)[None]).to(torch.int32))
+    be = DenseBackend(rtp, kvp)
+    q_all = torch.randn((L, B, H, D), generator=gen, device=dev).to(torch.bfloat16)
+    k_new = torch.randn((L, B, KV, D), generator=gen, device=dev).to(torch.bfloat16)
+    v_new = torch.randn((L, B, KV, D), generator=gen, device=dev).to(torch.bfloat16)
+    layers = [Layer(i, D**-0.5) for i in range(L)]
+    seq_lens = torch.full((B,), S, device=dev, dtype=torch.int64)
+    out_loc = torch.empty(B, device=dev, dtype=torch.int64)
+    batch = ForwardBatch(ForwardMode.DECODE, None, None, torch.arange(B, device=dev), seq_lens, out_loc, rtp, kvp, be)
+    torch.cuda.synchronize()
+    setup_s = time.perf_counter() - t_setup
+
+    def step():
+        torch.add(base, seq_lens - 1, out=out_loc)
+        for layer in range(L):
+            be.forward_decode(q_all[layer], k_new[layer], v_new[layer], layers[layer], batch)
+        seq_lens.add_(1)
+
+    step()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        graph.replay()
+    torch.cuda.synchronize()
+    us_per_layer_step = (time.perf_counter() - t0) * 1e6 / args.steps / L
+    seq_mid = S + 1 + args.warmup + args.steps // 2
+    kv_bytes = B * seq_mid * 2 * KV * D * 2
+    line = {
+        "metric": "µs per dense decode layer-step @128K ctx, batch 16 (comparator of the Quest layer step)",
+        "value": round(us_per_layer_step, 2),
+        "unit": "us per layer-step",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "higher_is_better": False,
+        "dtype": "bf16",
+        "data": "synthetic N(0,1) q/k/v, fixed seeds",
+        "config": {"workload": f"dense decode, batch {B}, {S}-token context, {L} layers cycled, "
+                               f"32q/4kv heads x 128", "batch": B, "seq_len": S, "layers": L},
+        "algorithmic_bytes_per_layer_step": kv_bytes,
+        "hbm_frac_layer_step": round(kv_bytes / (us_per_layer_step * 1e-6) / (HBM_PEAK_GBS * 1e9), 4),
+        "setup_s": round(setup_s, 1),
+    }
+    print(json.dumps(line))
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -249,6 +327,9 @@ def main() -> int:
                     help="contexts drawn uniform in [8192, ctx] per request (seeded) instead of all ctx")
     ap.add_argument("--hisparse", action="store_true", help="measure the quest_hisparse tier instead")
     ap.add_argument("--hisparse-layers", type=int, default=4)
+    ap.add_argument("--dense", action="store_true",
+                    help="measure dense decode (every request attends its whole context) instead")
+    ap.add_argument("--dense-layers", type=int, default=8, help="K/V pools of the dense run (cycled)")
     args = ap.parse_args()
     if args.copy_calibration:
         n = args.copy_calibration << 20
@@ -266,6 +347,8 @@ def main() -> int:
         return 2
     if args.hisparse:
         return hisparse_bench(args)
+    if args.dense:
+        return dense_bench(args)
 
     from qwenquest_amd import _lib
     from qwenquest_amd.attention.quest_only import QuestOnlyBackend

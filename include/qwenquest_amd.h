@@ -232,6 +232,30 @@ int qq_quest_forward_decode_phase(const void* q, int q_dtype, int64_t q_batch_st
                                   int64_t workspace_bytes, void* sync, int64_t sync_bytes, int phase,
                                   void* stream);
 
+/* Replaces DenseBackend.forward_decode (src/qwenquest/attention/dense.py:26-42) for
+ * one layer: the new tokens' K/V (k_new/v_new [bs, KV, D]; NULL: none) go to rows
+ * out_cache_loc (memory.py:114-120), then request i attends
+ * req_to_token[req_pool_indices[i], 0 .. seq_lens[i]) (ops.py:48-66) -> out
+ * [bs, H*D].  bf16 queries and K/V, KV*D = 4*128, H/KV <= 16 (QQ_EINVAL
+ * otherwise); seq_lens[i] <= req_to_token_stride.  sync as for
+ * qq_quest_forward_decode (>= qq_quest_layer_step_sync_bytes(bs, 4), zeroed
+ * once, left zeroed); workspace >= qq_dense_decode_workspace_bytes(bs,
+ * req_to_token_stride, H, KV).  Two launches: the K/V store, then the
+ * attention (per (request, KV head, part of at most 4096 rows), parts merged
+ * inside the launch). */
+int qq_dense_forward_decode(const void* q, int q_dtype, int64_t q_batch_stride, int num_q_heads,
+                            const void* k_new, const void* v_new, int new_dtype,
+                            const int64_t* out_cache_loc, void* k_layer, void* v_layer, int kv_dtype,
+                            int64_t kv_rows, int kv_heads, int head_dim,
+                            const int64_t* req_pool_indices, const int64_t* seq_lens, int bs,
+                            const int32_t* req_to_token, int64_t req_to_token_stride,
+                            int64_t req_to_token_rows, float scale, void* out, void* workspace,
+                            int64_t workspace_bytes, void* sync, int64_t sync_bytes, void* stream);
+
+/* Workspace bytes of qq_dense_forward_decode for contexts of up to max_rows
+ * tokens (no counterpart in the reference). */
+int64_t qq_dense_decode_workspace_bytes(int bs, int64_t max_rows, int num_q_heads, int kv_heads);
+
 /* Replaces MHATokenToKVPool.set_kv_buffer (src/qwenquest/memory.py:114-120):
  * k_layer[locs[i]] = k[i], v_layer[locs[i]] = v[i] (row = KV*D elements),
  * converting src_dtype -> buf_dtype. */

@@ -66,6 +66,12 @@ SIGNATURES: dict[str, tuple] = {
          _I, _I, _I, _P, _L, _L, _F, _P, _P, _P, _P, _L, _P, _L, _I, _P],
     ),
     "qq_quest_layer_step_sync_bytes": (_L, [_I, _I]),
+    "qq_dense_forward_decode": (
+        _I,
+        [_P, _I, _L, _I, _P, _P, _I, _P, _P, _P, _I, _L, _I, _I, _P, _P, _I, _P, _L, _L, _F, _P, _P, _L,
+         _P, _L, _P],
+    ),
+    "qq_dense_decode_workspace_bytes": (_L, [_I, _L, _I, _I]),
     "qq_kv_scatter": (_I, [_P, _P, _I, _L, _P, _P, _I, _P, _I, _L, _P]),
     "qq_hisparse_swap_in": (
         _I,

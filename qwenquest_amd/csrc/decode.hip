@@ -197,9 +197,8 @@ __global__ __launch_bounds__(64 * kHeadWaves, 1) void quest_attend_part_kernel(S
   const int per_wave = a.per_wave;
   const int per_block = kHeadWaves * per_wave;  // <= kStepMaxTopK
   const int slot_base = part * per_block;
-  if (!ROWS && long_b && slot_base < k * P) {  // block-uniform: this block attends selected pages
-    static_assert(ROWS || KPT > 0, "selection capacity");
-    constexpr int kSel = KPT > 0 ? KPT : 1;
+  if constexpr (KPT > 0) if (long_b && slot_base < k * P) {  // block-uniform: this block attends selected pages
+    constexpr int kSel = KPT;
     SelectSmem<kSel, kThreads>& ss = *reinterpret_cast<SelectSmem<kSel, kThreads>*>(smem_raw);
     const int lim = (req >= 0 && req < sa.R) ? min(sa.limit[b], sa.MP) : 0;
     const float* sc = sa.scores + (int64_t)b * sa.MP;
@@ -213,7 +212,7 @@ __global__ __launch_bounds__(64 * kHeadWaves, 1) void quest_attend_part_kernel(S
     if (tid < k) s_pages[tid] = ss.order[tid];
     __syncthreads();  // the list is in s_pages before the row table reuses the LDS
   }
-  int32_t* pos_out = !ROWS && h == 0 ? sa.positions + (int64_t)b * top_k : nullptr;
+  int32_t* pos_out = !ROWS && h == 0 && sa.positions ? sa.positions + (int64_t)b * top_k : nullptr;
   for (int i0 = 0; i0 < per_block; i0 += kThreads * 4) {
     int64_t pv[4];
     int64_t rv[4];
@@ -335,38 +334,75 @@ __global__ __launch_bounds__(64 * kHeadWaves, 1) void quest_attend_part_kernel(S
   __syncthreads();
   if (!s_last) return;
   if (tid == 0) st_agent(attn_count(a, bh), 0u);
-  // merge the parts: each thread one head x 4 channels, all loads in flight at once
+  // merge the parts (in part order: the maximum of the parts' m first, then the
+  // weighted sums): each thread one head x 4 channels; up to kMaxParts parts all
+  // loads in flight at once, more parts (dense decode) in two passes of groups
   const int64_t part0 = (int64_t)bh * parts;
   const __amdgpu_buffer_rsrc_t ro =
       agent_rsrc(a.part_o + part0 * G * kMfmaDim, (uint32_t)(parts * G * kMfmaDim * sizeof(float)));
   const uint64_t* ml64 = reinterpret_cast<const uint64_t*>(a.part_ml) + part0 * G;
   for (int grp = tid; grp < G * (kMfmaDim / 4); grp += kThreads) {
     const int head = grp >> 5, d4 = (grp & 31) * 4;
-    float4 ov[kMaxParts];
-    uint64_t mlv[kMaxParts];
-#pragma unroll
-    for (int j = 0; j < kMaxParts; ++j) {
-      if (j < parts) {
-        ov[j] = ld_agent_x4(ro, (uint32_t)(((j * G + head) * kMfmaDim + d4) * sizeof(float)));
-        mlv[j] = ld_agent(ml64 + j * G + head);
-      }
-    }
     float Mx = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < kMaxParts; ++j)
-      if (j < parts) Mx = fmaxf(Mx, __uint_as_float((uint32_t)mlv[j]));
     float Ls = 0.0f;
     float4 Os = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (parts <= kMaxParts) {
+      float4 ov[kMaxParts];
+      uint64_t mlv[kMaxParts];
 #pragma unroll
-    for (int j = 0; j < kMaxParts; ++j) {
-      if (j < parts) {
-        const float mj = __uint_as_float((uint32_t)mlv[j]);
-        const float wgt = mj == -INFINITY ? 0.0f : exp2f(mj - Mx);
-        Ls += wgt * __uint_as_float((uint32_t)(mlv[j] >> 32));
-        Os.x += wgt * ov[j].x;
-        Os.y += wgt * ov[j].y;
-        Os.z += wgt * ov[j].z;
-        Os.w += wgt * ov[j].w;
+      for (int j = 0; j < kMaxParts; ++j) {
+        if (j < parts) {
+          ov[j] = ld_agent_x4(ro, (uint32_t)(((j * G + head) * kMfmaDim + d4) * sizeof(float)));
+          mlv[j] = ld_agent(ml64 + j * G + head);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < kMaxParts; ++j)
+        if (j < parts) Mx = fmaxf(Mx, __uint_as_float((uint32_t)mlv[j]));
+#pragma unroll
+      for (int j = 0; j < kMaxParts; ++j) {
+        if (j < parts) {
+          const float mj = __uint_as_float((uint32_t)mlv[j]);
+          const float wgt = mj == -INFINITY ? 0.0f : exp2f(mj - Mx);
+          Ls += wgt * __uint_as_float((uint32_t)(mlv[j] >> 32));
+          Os.x += wgt * ov[j].x;
+          Os.y += wgt * ov[j].y;
+          Os.z += wgt * ov[j].z;
+          Os.w += wgt * ov[j].w;
+        }
+      }
+    } else {
+      for (int j0 = 0; j0 < parts; j0 += kMaxParts) {
+        uint64_t mlv[kMaxParts];
+#pragma unroll
+        for (int j = 0; j < kMaxParts; ++j)
+          if (j0 + j < parts) mlv[j] = ld_agent(ml64 + (j0 + j) * G + head);
+#pragma unroll
+        for (int j = 0; j < kMaxParts; ++j)
+          if (j0 + j < parts) Mx = fmaxf(Mx, __uint_as_float((uint32_t)mlv[j]));
+      }
+      for (int j0 = 0; j0 < parts; j0 += kMaxParts) {
+        float4 ov[kMaxParts];
+        uint64_t mlv[kMaxParts];
+#pragma unroll
+        for (int j = 0; j < kMaxParts; ++j) {
+          if (j0 + j < parts) {
+            ov[j] = ld_agent_x4(ro, (uint32_t)((((j0 + j) * G + head) * kMfmaDim + d4) * sizeof(float)));
+            mlv[j] = ld_agent(ml64 + (j0 + j) * G + head);
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < kMaxParts; ++j) {
+          if (j0 + j < parts) {
+            const float mj = __uint_as_float((uint32_t)mlv[j]);
+            const float wgt = mj == -INFINITY ? 0.0f : exp2f(mj - Mx);
+            Ls += wgt * __uint_as_float((uint32_t)(mlv[j] >> 32));
+            Os.x += wgt * ov[j].x;
+            Os.y += wgt * ov[j].y;
+            Os.z += wgt * ov[j].z;
+            Os.w += wgt * ov[j].w;
+          }
+        }
       }
     }
     const bool any = Ls > 0.0f;
@@ -483,6 +519,80 @@ int qq::attend_rows_fused(const void* q, int64_t q_bstride, int num_q_heads, con
   a.actual = actual;
   quest_attend_part_kernel<true, 0><<<bs * kStepKV * parts, 64 * kHeadWaves, head_smem_bytes<true, 0>(), s>>>(a);
   return QQ_OK;
+}
+
+// Dense decode (attention/dense.py:26-42): every request attends
+// req_to_token[req, 0 .. seq_len) - the fused attention kernel without a
+// selection (its dense layout), at most kStepMaxTopK rows per block and as
+// many parts per (request, KV head) as the longest context of the table needs.
+static int dense_parts(int64_t max_rows) { return max(1, ceil_div(max_rows, kStepMaxTopK)); }
+
+extern "C" int64_t qq_dense_decode_workspace_bytes(int bs, int64_t max_rows, int num_q_heads, int kv_heads) {
+  if (bs <= 0 || max_rows <= 0 || kv_heads <= 0 || num_q_heads <= 0) return 0;
+  const int parts = dense_parts(max_rows);
+  return parts > 1 ? (int64_t)bs * kv_heads * parts * (num_q_heads / kv_heads) * (kMfmaDim + 2) *
+                         (int64_t)sizeof(float)
+                   : 0;
+}
+
+extern "C" int qq_dense_forward_decode(const void* q, int q_dtype, int64_t q_batch_stride, int num_q_heads,
+                                       const void* k_new, const void* v_new, int new_dtype,
+                                       const int64_t* out_cache_loc, void* k_layer, void* v_layer, int kv_dtype,
+                                       int64_t kv_rows, int kv_heads, int head_dim, const int64_t* req_pool_indices,
+                                       const int64_t* seq_lens, int bs, const int32_t* req_to_token,
+                                       int64_t req_to_token_stride, int64_t req_to_token_rows, float scale,
+                                       void* out, void* workspace, int64_t workspace_bytes, void* sync,
+                                       int64_t sync_bytes, void* stream) {
+  const char* what = "qq_dense_forward_decode";
+  QQ_REQUIRE(q_dtype == QQ_DTYPE_BF16 && kv_dtype == QQ_DTYPE_BF16 && (!k_new || new_dtype == QQ_DTYPE_BF16) &&
+                 kv_heads == kStepKV && head_dim == kMfmaDim && num_q_heads % kv_heads == 0 &&
+                 num_q_heads / kv_heads <= kStepMaxG,
+             "%s: the HIP dense decode takes bf16 queries and K/V, %d KV heads x %d, at most %d query heads "
+             "per KV head", what, kStepKV, kMfmaDim, kStepMaxG);
+  QQ_REQUIRE(bs >= 0 && req_to_token_stride > 0 && req_to_token_stride <= (int64_t)1 << 30, "%s: bad sizes", what);
+  QQ_REQUIRE(!k_new || (v_new && out_cache_loc), "%s: new K without V or locations", what);
+  if (bs == 0) return QQ_OK;
+  QQ_REQUIRE(q && k_layer && v_layer && req_pool_indices && seq_lens && req_to_token && out, "%s: null pointer", what);
+  QQ_REQUIRE(sync && sync_bytes >= qq_quest_layer_step_sync_bytes(bs, kv_heads), "%s: sync buffer too small", what);
+  const int64_t need = qq_dense_decode_workspace_bytes(bs, req_to_token_stride, num_q_heads, kv_heads);
+  QQ_REQUIRE(need == 0 || (workspace && workspace_bytes >= need), "%s: workspace %lld bytes < %lld needed", what,
+             (long long)workspace_bytes, (long long)need);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (k_new) {  // set_kv_buffer (memory.py:114-120) before the attention reads the pool
+    const int st = qq_kv_scatter(k_layer, v_layer, kv_dtype, kv_rows, k_new, v_new, new_dtype, out_cache_loc, bs,
+                                 (int64_t)kv_heads * head_dim, stream);
+    if (st != QQ_OK) return st;
+  }
+  const int top_k = (int)req_to_token_stride;  // every context fits: seq_len <= the table's width
+  const int G = num_q_heads / kv_heads;
+  const int parts = dense_parts(top_k);
+  StepArgs a{};
+  a.s.q = q;
+  a.s.q_dtype = QQ_DTYPE_BF16;
+  a.s.q_bstride = q_batch_stride;
+  a.s.H = num_q_heads;
+  a.s.rpi = req_pool_indices;
+  a.s.seq = seq_lens;
+  a.s.top_k = top_k;
+  a.s.P = 64;
+  a.s.k_sel = 0;  // no selection: positions 0 .. seq_len - 1
+  a.k = static_cast<const uint16_t*>(k_layer);
+  a.v = static_cast<const uint16_t*>(v_layer);
+  a.kv_rows = kv_rows;
+  a.r2t = req_to_token;
+  a.r2t_stride = req_to_token_stride;
+  a.r2t_rows = req_to_token_rows;
+  a.sl2 = scale * kLog2e;
+  a.out = static_cast<uint16_t*>(out);
+  a.part_o = static_cast<float*>(workspace);
+  a.part_ml = a.part_o + (int64_t)bs * kStepKV * parts * G * kMfmaDim;
+  a.sync = static_cast<uint32_t*>(sync);
+  a.bs = bs;
+  a.G = G;
+  a.parts = parts;
+  a.per_wave = ceil_div(top_k, parts * kHeadWaves * 32) * 32;
+  quest_attend_part_kernel<false, 0><<<bs * kStepKV * parts, 64 * kHeadWaves, head_smem_bytes<false, 0>(), s>>>(a);
+  return check_launch(what);
 }
 
 static int forward_decode(
