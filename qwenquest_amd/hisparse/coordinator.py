@@ -24,7 +24,7 @@ from dataclasses import dataclass
 import torch
 
 from qwenquest_amd import _lib
-from qwenquest_amd.memory import MHATokenToKVPool, TokenToKVPoolAllocator
+from qwenquest_amd.memory import MHATokenToKVPool, TokenToKVPoolAllocator, kv_pair_zeros
 from qwenquest_amd.quest import QuestAlgorithm
 
 __all__ = ["HiSparseCoordinator", "SwapInStats"]
@@ -99,8 +99,7 @@ class HiSparseCoordinator:
 
         # ---- device tier: per request buf LRU slots + 1 newest-token slot
         dshape = (num_layers, max_reqs * (buf + 1), kv_heads, head_dim)
-        self.device_k_all = torch.zeros(dshape, dtype=dtype, device=self.device)
-        self.device_v_all = torch.zeros(dshape, dtype=dtype, device=self.device)
+        self.device_k_all, self.device_v_all = kv_pair_zeros(dshape, dtype, self.device)
         self.device_k = list(self.device_k_all.unbind(0))
         self.device_v = list(self.device_v_all.unbind(0))
         self.req_to_device_buffer = torch.arange(max_reqs * (buf + 1), dtype=torch.int64,
