@@ -8,24 +8,28 @@
 //   1. page scores of every long request (score_pages_fast_kernel, one block
 //      per (request, 32 candidate pages), all CUs) and the new token's K/V
 //      (set_kv_buffer, memory.py:114-120).
-//   2. attention, one block per (request, KV head, part of the rows), enough
-//      parts to put one block on every CU: the block selects its request's
-//      pages from the scores (filter top-k; every block of a request computes
-//      the same list, so no block waits on another), turns its share of the
-//      list into layout positions and pool rows (req_to_token,
-//      quest_only.py:149-151) in LDS - the KV-head-0 blocks also write the
-//      positions - then each of its 8 waves streams its rows in steps of 32
-//      with 2 steps in flight and an online softmax (MFMA QK^T and PV), and
-//      the waves combine in LDS.  The parts' (m, l, o) partials go out with
-//      agent-scope stores; the block that completes a (request, KV head)
-//      count merges them into the output.
+//   2. attention, one 4-wave block per (request, KV head, part of the rows),
+//      up to 8 parts (512 blocks at batch 16, two per CU): the block selects
+//      its request's pages from the scores (filter top-k; every block of a
+//      request computes the same list, so no block waits on another), turns
+//      its share of the list into layout positions and pool rows
+//      (req_to_token, quest_only.py:149-151) in LDS - the KV-head-0 blocks
+//      also write the positions - then each of its 4 waves streams its rows in
+//      steps of 16 with an online softmax (MFMA QK^T and PV) at no more than
+//      128 VGPRs, and the waves combine in LDS.  The parts' (m, l, o) partials
+//      go out with agent-scope stores; the block that completes a (request,
+//      KV head) count merges them into the output.
 // The counters return to zero before the launch ends, so the next call (or a
 // graph replay) starts clean.  A CU streams only ~30-40 GB/s of these 256-byte
-// row slices, so the attention grid covers every CU.
+// row slices, so the attention grid covers every CU.  quest_hisparse's
+// attention over its hot-buffer rows runs the same blocks, so both backends
+// compute the same partials in the same order.
 //
 // Other shapes: four launches on one stream, each consuming the previous one's
 // output: score (all CUs) -> select + new-token store (one block per request)
 // -> chunk attention (MFMA) -> merge.
+#include <algorithm>
+
 #include "qq_quest_dev.h"
 
 namespace qq {
@@ -35,9 +39,17 @@ constexpr int kStepKV = 4;            // KV heads of the fused path (KV*D = 512)
 constexpr int kStepMaxG = 16;
 constexpr int kMaxSelFused = 64;
 constexpr int kStepMaxTopK = 4096;
-constexpr int kHeadWaves = 8;        // attention block: 8 waves (two per SIMD)
-constexpr int kHeadDepth = 2;        // steps of 32 rows in flight per wave
-constexpr int kMaxParts = 8;         // attention blocks per (request, KV head)
+constexpr int kHeadWaves = 8;        // dense decode: 8-wave blocks (two waves per SIMD)
+constexpr int kHeadTiles = 2;        // 16-row tiles per step (32 rows)
+constexpr int kHeadDepth = 2;        // steps in flight per wave
+constexpr int kMaxParts = 8;         // dense decode: parts merged in one pass
+// The Quest step's attention: 4-wave blocks (at most 128 VGPRs, four per CU),
+// up to kW4Parts per (request, KV head); a wave streams 16-row steps one at a
+// time and a block's row table holds up to kW4RowCap slots (top_k <= 4096
+// needs at most 512).
+constexpr int kW4Waves = 4;
+constexpr int kW4Parts = 8;
+constexpr int kW4RowCap = 1024;
 
 struct StepArgs {
   SelectArgs s;            // scoring, selection, positions, new token
@@ -63,45 +75,48 @@ __device__ inline uint32_t* attn_count(const StepArgs& a, int bh) { return a.syn
 
 __device__ inline bool needs_selection(const SelectArgs& sa, int64_t s) { return s > sa.top_k && sa.k_sel > 0; }
 
-// One wave's step: the K and V slices of 32 layout rows of one KV head
+// One wave's step: the K and V slices of 16T layout rows of one KV head
 // (lane layouts of attn_wave64: K tile t = tokens 16t .. 16t+15, V k-step u =
 // tokens 16u .. 16u+15).
+template <int T>
 struct StepRegs {
-  bf16x8_t ka[2][4];
-  uint4 vr[2][4];
+  bf16x8_t ka[T][4];
+  uint4 vr[T][4];
 };
 
-__device__ inline void load_step(StepRegs& r, const int32_t* rows, int t0, const uint16_t* kb, const uint16_t* vb,
+template <int T>
+__device__ inline void load_step(StepRegs<T>& r, const int32_t* rows, int t0, const uint16_t* kb, const uint16_t* vb,
                                  int lo, int hi) {
   constexpr int kRow = kStepKV * kMfmaDim;
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
+  for (int t = 0; t < T; ++t) {
     const uint16_t* kp = kb + (int64_t)rows[t0 + t * 16 + lo] * kRow + hi * 8;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) r.ka[t][ks] = *reinterpret_cast<const bf16x8_t*>(kp + ks * 32);
   }
 #pragma unroll
-  for (int u = 0; u < 2; ++u)
+  for (int u = 0; u < T; ++u)
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       r.vr[u][j] = *reinterpret_cast<const uint4*>(vb + (int64_t)rows[t0 + u * 16 + hi * 4 + j] * kRow + lo * 8);
 }
 
-// Online-softmax update with one step (tokens t0 .. t0+31, the first `valid`
-// of them real): M, L per head lo (log2 units), o[e][i] per (head 4hi+i,
-// channel 8lo+e).
-__device__ inline void attend_step(const StepRegs& r, const bf16x8_t (&qb)[4], int valid, float sl2, float& M,
+// Online-softmax update with one step (tokens t0 .. t0+16T-1, the first
+// `valid` of them real): M, L per head lo (log2 units), o[e][i] per (head
+// 4hi+i, channel 8lo+e).
+template <int T>
+__device__ inline void attend_step(const StepRegs<T>& r, const bf16x8_t (&qb)[4], int valid, float sl2, float& M,
                                    float& L, float4_t (&o)[8], int lo, int hi) {
-  float4_t acc[2];
+  float4_t acc[T];
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
+  for (int t = 0; t < T; ++t) {
     acc[t] = float4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(r.ka[t][ks], qb[ks], acc[t], 0, 0, 0);
   }
   float mx = -INFINITY;
 #pragma unroll
-  for (int t = 0; t < 2; ++t)
+  for (int t = 0; t < T; ++t)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const float x = (t * 16 + hi * 4 + i) < valid ? acc[t][i] * sl2 : -INFINITY;
@@ -114,9 +129,9 @@ __device__ inline void attend_step(const StepRegs& r, const bf16x8_t (&qb)[4], i
   const float Mn = fmaxf(M, mx);
   const float alpha = M == -INFINITY ? 0.0f : exp2f(M - Mn);  // rescale of the running sums
   float sum = 0.0f;
-  short4_t pa[2];
+  short4_t pa[T];
 #pragma unroll
-  for (int t = 0; t < 2; ++t)
+  for (int t = 0; t < T; ++t)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const uint16_t pb = Mn == -INFINITY ? (uint16_t)0 : f2bf(exp2f(acc[t][i] - Mn));
@@ -135,7 +150,7 @@ __device__ inline void attend_step(const StepRegs& r, const bf16x8_t (&qb)[4], i
     for (int e = 0; e < 8; ++e) o[e][i] *= ai;
   }
 #pragma unroll
-  for (int u = 0; u < 2; ++u) {
+  for (int u = 0; u < T; ++u) {
     short4_t vbv[8];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -152,37 +167,37 @@ __device__ inline void attend_step(const StepRegs& r, const bf16x8_t (&qb)[4], i
   }
 }
 
+template <int W, int ROWCAP>
 struct HeadSmem {
-  int32_t rows[kStepMaxTopK];  // this block's layout slots -> pool rows
-  float m[kHeadWaves][kStepMaxG];
-  float l[kHeadWaves][kStepMaxG];
-  float o[kHeadWaves][kStepMaxG][kMfmaDim];
+  int32_t rows[ROWCAP];  // this block's layout slots -> pool rows
+  float m[W][kStepMaxG];
+  float l[W][kStepMaxG];
+  float o[W][kStepMaxG][kMfmaDim];
 };
 
-// Attention of one (request, KV head, part): the block's share of the layout
-// slots, per_wave rows per wave in steps of 32 (kHeadDepth in flight), the
-// waves combined in LDS.  With one part the block writes the output; else it
-// stores an (m, l, o) partial (agent scope) and the block that completes the
-// (request, KV head) count merges the parts.  ROWS: the pool rows of the slots
-// are given (rows_in, actual) instead of coming from the page list and
+// Attention of one (request, KV head, part) by a block of W waves: the block's
+// share of the layout slots, per_wave rows per wave in steps of 16T rows
+// (DEPTH steps in flight), the waves combined in LDS.  With one part the
+// block writes the output; else it stores an (m, l, o) partial (agent scope)
+// and the block that completes the (request, KV head) count merges the parts
+// (up to MG at once; GROUPED: more in groups).  ROWS: the pool rows of the
+// slots are given (rows_in, actual) instead of coming from the page list and
 // req_to_token - the same arithmetic over the same slot order.  Otherwise the
 // block first selects its request's pages itself (quest.py:450-452) from the
-// scores of the scoring launch - every block of the request computes the same
-// list - with a KPT x 512-page selection that aliases the LDS the row table
-// and the wave combine use later.
-template <bool ROWS, int KPT>
-__global__ __launch_bounds__(64 * kHeadWaves, 1) void quest_attend_part_kernel(StepArgs a) {
-  extern __shared__ __align__(16) unsigned char smem_raw[];
-  HeadSmem& sm = *reinterpret_cast<HeadSmem*>(smem_raw);
-  __shared__ uint32_t s_last;
-  __shared__ int32_t s_pages[kMaxSelFused];
+// page scores - every block of the request computes the same list - with a
+// KPT x 64W-page selection that aliases the LDS the row table and the wave
+// combine use later.
+template <bool ROWS, int KPT, int W, int T, int DEPTH, int MG, bool GROUPED, int ROWCAP>
+__device__ inline void attend_item(const StepArgs& a, int bh, int part, unsigned char* smem_raw, uint32_t* s_last,
+                                   int32_t* s_pages) {
+  using Smem = HeadSmem<W, ROWCAP>;
+  Smem& sm = *reinterpret_cast<Smem*>(smem_raw);
   const SelectArgs& sa = a.s;
-  constexpr int kThreads = 64 * kHeadWaves;
+  constexpr int kThreads = 64 * W;
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   const int lo = lane & 15, hi = lane >> 4;
   const int parts = a.parts;
-  const int bh = blockIdx.x / parts, part = blockIdx.x - bh * parts;
   const int b = bh / kStepKV, h = bh - b * kStepKV;
   const int64_t s = ROWS ? 0 : sa.seq[b];
   const int64_t req = ROWS ? 0 : sa.rpi[b];
@@ -195,20 +210,19 @@ __global__ __launch_bounds__(64 * kHeadWaves, 1) void quest_attend_part_kernel(S
   // the 32-row step; the row table is filled over the whole range (row 0 past n),
   // so every row a step reads is initialised and in range
   const int per_wave = a.per_wave;
-  const int per_block = kHeadWaves * per_wave;  // <= kStepMaxTopK
+  const int per_block = W * per_wave;  // <= ROWCAP
   const int slot_base = part * per_block;
   if constexpr (KPT > 0) if (long_b && slot_base < k * P) {  // block-uniform: this block attends selected pages
-    constexpr int kSel = KPT;
-    SelectSmem<kSel, kThreads>& ss = *reinterpret_cast<SelectSmem<kSel, kThreads>*>(smem_raw);
+    SelectSmem<KPT, kThreads>& ss = *reinterpret_cast<SelectSmem<KPT, kThreads>*>(smem_raw);
     const int lim = (req >= 0 && req < sa.R) ? min(sa.limit[b], sa.MP) : 0;
     const float* sc = sa.scores + (int64_t)b * sa.MP;
-    float sv[kSel];
+    float sv[KPT];
 #pragma unroll
-    for (int i = 0; i < kSel; ++i) {
+    for (int i = 0; i < KPT; ++i) {
       const int p = tid + kThreads * i;
       sv[i] = p < lim ? sc[p] : 0.0f;
     }
-    select_topk_block<kSel, kThreads>(sv, lim, max(lim, k), k, ss);
+    select_topk_block<KPT, kThreads>(sv, lim, max(lim, k), k, ss);
     if (tid < k) s_pages[tid] = ss.order[tid];
     __syncthreads();  // the list is in s_pages before the row table reuses the LDS
   }
@@ -264,27 +278,28 @@ __global__ __launch_bounds__(64 * kHeadWaves, 1) void quest_attend_part_kernel(S
   // the row table is in LDS; the position stores and query loads stay in flight
   lds_barrier();
   // this wave's rows: local [r0, r0 + per_wave), real up to slot n
+  constexpr int kStep = 16 * T;
   const int r0 = wave * per_wave;
   const int r_end = max(r0, min(r0 + per_wave, n - slot_base));
-  const int nsteps = (r_end - r0 + 31) / 32;
+  const int nsteps = (r_end - r0 + kStep - 1) / kStep;
   const uint16_t* kb = a.k + h * kMfmaDim;
   const uint16_t* vb = a.v + h * kMfmaDim;
   float M = -INFINITY, L = 0.0f;
   float4_t o[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) o[e] = float4_t{0.f, 0.f, 0.f, 0.f};
-  StepRegs ring[kHeadDepth];
+  StepRegs<T> ring[DEPTH];
 #pragma unroll
-  for (int j = 0; j < kHeadDepth - 1; ++j)
-    if (j < nsteps) load_step(ring[j], sm.rows, r0 + 32 * j, kb, vb, lo, hi);
-  for (int i0 = 0; i0 < nsteps; i0 += kHeadDepth) {
+  for (int j = 0; j < DEPTH - 1; ++j)
+    if (j < nsteps) load_step<T>(ring[j], sm.rows, r0 + kStep * j, kb, vb, lo, hi);
+  for (int i0 = 0; i0 < nsteps; i0 += DEPTH) {
 #pragma unroll
-    for (int j = 0; j < kHeadDepth; ++j) {
+    for (int j = 0; j < DEPTH; ++j) {
       const int i = i0 + j;
       if (i >= nsteps) break;
-      const int ahead = i + kHeadDepth - 1;
-      if (ahead < nsteps) load_step(ring[(j + kHeadDepth - 1) % kHeadDepth], sm.rows, r0 + 32 * ahead, kb, vb, lo, hi);
-      attend_step(ring[j], qb, r_end - (r0 + 32 * i), a.sl2, M, L, o, lo, hi);
+      const int ahead = i + DEPTH - 1;
+      if (ahead < nsteps) load_step<T>(ring[(j + DEPTH - 1) % DEPTH], sm.rows, r0 + kStep * ahead, kb, vb, lo, hi);
+      attend_step<T>(ring[j], qb, r_end - (r0 + kStep * i), a.sl2, M, L, o, lo, hi);
     }
   }
   // combine the waves in LDS
@@ -308,10 +323,10 @@ __global__ __launch_bounds__(64 * kHeadWaves, 1) void quest_attend_part_kernel(S
     const int head = idx >> 7, d = idx & 127;
     float Mx = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kHeadWaves; ++w) Mx = fmaxf(Mx, sm.m[w][head]);
+    for (int w = 0; w < W; ++w) Mx = fmaxf(Mx, sm.m[w][head]);
     float Ls = 0.0f, Os = 0.0f;
 #pragma unroll
-    for (int w = 0; w < kHeadWaves; ++w) {
+    for (int w = 0; w < W; ++w) {
       const float mw = sm.m[w][head];
       const float wgt = mw == -INFINITY ? 0.0f : exp2f(mw - Mx);
       Ls += wgt * sm.l[w][head];
@@ -330,13 +345,13 @@ __global__ __launch_bounds__(64 * kHeadWaves, 1) void quest_attend_part_kernel(S
   if (parts == 1) return;
   wait_memory();
   __syncthreads();
-  if (tid == 0) s_last = add_agent(attn_count(a, bh), 1u) == (uint32_t)(parts - 1);
+  if (tid == 0) *s_last = add_agent(attn_count(a, bh), 1u) == (uint32_t)(parts - 1);
   __syncthreads();
-  if (!s_last) return;
+  if (!*s_last) return;
   if (tid == 0) st_agent(attn_count(a, bh), 0u);
   // merge the parts (in part order: the maximum of the parts' m first, then the
-  // weighted sums): each thread one head x 4 channels; up to kMaxParts parts all
-  // loads in flight at once, more parts (dense decode) in two passes of groups
+  // weighted sums): each thread one head x 4 channels; up to MG parts all loads
+  // in flight at once, more parts (dense decode) in two passes of groups
   const int64_t part0 = (int64_t)bh * parts;
   const __amdgpu_buffer_rsrc_t ro =
       agent_rsrc(a.part_o + part0 * G * kMfmaDim, (uint32_t)(parts * G * kMfmaDim * sizeof(float)));
@@ -346,21 +361,21 @@ __global__ __launch_bounds__(64 * kHeadWaves, 1) void quest_attend_part_kernel(S
     float Mx = -INFINITY;
     float Ls = 0.0f;
     float4 Os = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (parts <= kMaxParts) {
-      float4 ov[kMaxParts];
-      uint64_t mlv[kMaxParts];
+    if (!GROUPED || parts <= MG) {
+      float4 ov[MG];
+      uint64_t mlv[MG];
 #pragma unroll
-      for (int j = 0; j < kMaxParts; ++j) {
+      for (int j = 0; j < MG; ++j) {
         if (j < parts) {
           ov[j] = ld_agent_x4(ro, (uint32_t)(((j * G + head) * kMfmaDim + d4) * sizeof(float)));
           mlv[j] = ld_agent(ml64 + j * G + head);
         }
       }
 #pragma unroll
-      for (int j = 0; j < kMaxParts; ++j)
+      for (int j = 0; j < MG; ++j)
         if (j < parts) Mx = fmaxf(Mx, __uint_as_float((uint32_t)mlv[j]));
 #pragma unroll
-      for (int j = 0; j < kMaxParts; ++j) {
+      for (int j = 0; j < MG; ++j) {
         if (j < parts) {
           const float mj = __uint_as_float((uint32_t)mlv[j]);
           const float wgt = mj == -INFINITY ? 0.0f : exp2f(mj - Mx);
@@ -372,27 +387,27 @@ __global__ __launch_bounds__(64 * kHeadWaves, 1) void quest_attend_part_kernel(S
         }
       }
     } else {
-      for (int j0 = 0; j0 < parts; j0 += kMaxParts) {
-        uint64_t mlv[kMaxParts];
+      for (int j0 = 0; j0 < parts; j0 += MG) {
+        uint64_t mlv[MG];
 #pragma unroll
-        for (int j = 0; j < kMaxParts; ++j)
+        for (int j = 0; j < MG; ++j)
           if (j0 + j < parts) mlv[j] = ld_agent(ml64 + (j0 + j) * G + head);
 #pragma unroll
-        for (int j = 0; j < kMaxParts; ++j)
+        for (int j = 0; j < MG; ++j)
           if (j0 + j < parts) Mx = fmaxf(Mx, __uint_as_float((uint32_t)mlv[j]));
       }
-      for (int j0 = 0; j0 < parts; j0 += kMaxParts) {
-        float4 ov[kMaxParts];
-        uint64_t mlv[kMaxParts];
+      for (int j0 = 0; j0 < parts; j0 += MG) {
+        float4 ov[MG];
+        uint64_t mlv[MG];
 #pragma unroll
-        for (int j = 0; j < kMaxParts; ++j) {
+        for (int j = 0; j < MG; ++j) {
           if (j0 + j < parts) {
             ov[j] = ld_agent_x4(ro, (uint32_t)((((j0 + j) * G + head) * kMfmaDim + d4) * sizeof(float)));
             mlv[j] = ld_agent(ml64 + (j0 + j) * G + head);
           }
         }
 #pragma unroll
-        for (int j = 0; j < kMaxParts; ++j) {
+        for (int j = 0; j < MG; ++j) {
           if (j0 + j < parts) {
             const float mj = __uint_as_float((uint32_t)mlv[j]);
             const float wgt = mj == -INFINITY ? 0.0f : exp2f(mj - Mx);
@@ -410,6 +425,35 @@ __global__ __launch_bounds__(64 * kHeadWaves, 1) void quest_attend_part_kernel(S
     const uint32_t hi2 = (uint32_t)f2bf(any ? Os.z / Ls : 0.0f) | ((uint32_t)f2bf(any ? Os.w / Ls : 0.0f) << 16);
     *reinterpret_cast<uint2*>(outp + head * kMfmaDim + d4) = make_uint2(lo2, hi2);
   }
+}
+
+using HeadSmemLaunch = HeadSmem<kHeadWaves, kStepMaxTopK>;
+using HeadSmemW4 = HeadSmem<kW4Waves, kW4RowCap>;
+
+// The attention launch of the fused layer step (and of the dense decode and
+// the attention over given rows): one 8-wave block per (request, KV head,
+// part), blockIdx = (request, KV head) * parts + part.
+template <bool ROWS, int KPT>
+__global__ __launch_bounds__(64 * kHeadWaves, 1) void quest_attend_part_kernel(StepArgs a) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  __shared__ uint32_t s_last;
+  __shared__ int32_t s_pages[kMaxSelFused];
+  const int bh = blockIdx.x / a.parts, part = blockIdx.x - bh * a.parts;
+  attend_item<ROWS, KPT, kHeadWaves, kHeadTiles, kHeadDepth, kMaxParts, true, kStepMaxTopK>(
+      a, bh, part, smem_raw, &s_last, s_pages);
+}
+
+// The Quest step's attention (after the score launch, and over given rows for
+// quest_hisparse, so that both compute the same partials in the same order):
+// one 4-wave block per (request, KV head, part), blockIdx = (request, KV head)
+// * parts + part.
+template <bool ROWS, int KPT>
+__global__ __launch_bounds__(64 * kW4Waves, 4) void quest_attend_w4_kernel(StepArgs a) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  __shared__ uint32_t s_last;
+  __shared__ int32_t s_pages[kMaxSelFused];
+  const int bh = blockIdx.x / a.parts, part = blockIdx.x - bh * a.parts;
+  attend_item<ROWS, KPT, kW4Waves, 1, 1, kW4Parts, false, kW4RowCap>(a, bh, part, smem_raw, &s_last, s_pages);
 }
 
 }  // namespace
@@ -439,20 +483,24 @@ static int device_cu_count() {
 // per device).
 template <bool ROWS, int KPT>
 static size_t head_smem_bytes() {
-  static_assert(sizeof(SelectSmem<(KPT > 0 ? KPT : 1), 64 * kHeadWaves>) <= sizeof(HeadSmem), "aliased LDS");
+  static_assert(sizeof(SelectSmem<(KPT > 0 ? KPT : 1), 64 * kHeadWaves>) <= sizeof(HeadSmemLaunch), "aliased LDS");
   static bool opted[64] = {false};
   int dev = 0;
   if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64 && !opted[dev]) {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&quest_attend_part_kernel<ROWS, KPT>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)sizeof(HeadSmem));
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)sizeof(HeadSmemLaunch));
     opted[dev] = true;
   }
-  return sizeof(HeadSmem);
+  return sizeof(HeadSmemLaunch);
 }
 
+// LDS: the row table and wave combine, or the selection (up to 24 x 256 pages)
+// that aliases them.
 template <int KPT>
 static void launch_attend_select(const StepArgs& a, int blocks, hipStream_t s) {
-  quest_attend_part_kernel<false, KPT><<<blocks, 64 * kHeadWaves, head_smem_bytes<false, KPT>(), s>>>(a);
+  constexpr size_t kSmem = std::max(sizeof(HeadSmemW4), sizeof(SelectSmem<KPT, 64 * kW4Waves>));
+  static_assert(kSmem <= 64 * 1024, "within the default LDS limit");
+  quest_attend_w4_kernel<false, KPT><<<blocks, 64 * kW4Waves, kSmem, s>>>(a);
 }
 
 // Shapes the fused layer step takes (bf16, KV*D = 4*128, G <= 16, page 64, at
@@ -465,14 +513,13 @@ static bool fused_shape(int q_dtype, int kv_dtype, int new_dtype, int num_q_head
     return false;
   return q_dtype == QQ_DTYPE_BF16 && kv_dtype == QQ_DTYPE_BF16 && (new_dtype < 0 || new_dtype == QQ_DTYPE_BF16) &&
          num_q_heads / kv_heads <= kStepMaxG && top_k / page_size - 1 <= kMaxSelFused && top_k <= kStepMaxTopK &&
-         max_pages <= 24 * kBlock;
+         max_pages <= 24 * 64 * kW4Waves;
 }
 
 // Attention blocks per (request, KV head) of the fused attention: enough to
 // cover every CU once (the blocks run one per CU), at least 32 rows per wave.
-static int step_parts(int bs, int kv_heads, int top_k) {
-  return max(1, min(kMaxParts, min(device_cu_count() / max(1, bs * kv_heads), ceil_div(top_k, kHeadWaves * 32))));
-}
+static int step_parts(int top_k) { return max(1, min(kW4Parts, ceil_div(top_k, kW4Waves * 32))); }
+static int step_per_wave(int top_k, int parts) { return ceil_div(top_k, parts * kW4Waves * 32) * 32; }
 
 extern "C" int qq_quest_fused_step(int q_dtype, int kv_dtype, int new_dtype, int num_q_heads, int kv_heads,
                                    int head_dim, int page_size, int top_k, int max_pages) {
@@ -492,7 +539,7 @@ int qq::attend_rows_fused(const void* q, int64_t q_bstride, int num_q_heads, con
     return 1;
   const int top_k = (int)slots;
   const int G = num_q_heads / kStepKV;
-  const int parts = step_parts(bs, kStepKV, top_k);
+  const int parts = step_parts(top_k);
   const int64_t part_bytes = (int64_t)bs * kStepKV * parts * G * (kMfmaDim + 2) * (int64_t)sizeof(float);
   if (parts > 1 && workspace_bytes < part_bytes) return 1;
   StepArgs a{};
@@ -510,14 +557,14 @@ int qq::attend_rows_fused(const void* q, int64_t q_bstride, int num_q_heads, con
   a.part_o = static_cast<float*>(workspace);
   a.part_ml = a.part_o + (int64_t)bs * kStepKV * parts * G * kMfmaDim;
   a.parts = parts;
-  a.per_wave = ceil_div(top_k, parts * kHeadWaves * 32) * 32;
+  a.per_wave = step_per_wave(top_k, parts);
   a.sync = static_cast<uint32_t*>(sync);
   a.bs = bs;
   a.G = G;
   a.rows_in = rows;
   a.rows_stride = slots;
   a.actual = actual;
-  quest_attend_part_kernel<true, 0><<<bs * kStepKV * parts, 64 * kHeadWaves, head_smem_bytes<true, 0>(), s>>>(a);
+  quest_attend_w4_kernel<true, 0><<<bs * kStepKV * parts, 64 * kW4Waves, sizeof(HeadSmemW4), s>>>(a);
   return QQ_OK;
 }
 
@@ -654,8 +701,8 @@ static int forward_decode(
   sa.pool_rows = kv_rows;
 
   const int G = num_q_heads / kv_heads;
-  const int parts = step_parts(bs, kv_heads, top_k);
-  const int per_wave = ceil_div(top_k, parts * kHeadWaves * 32) * 32;
+  const int parts = step_parts(top_k);
+  const int per_wave = step_per_wave(top_k, parts);
   const int64_t part_bytes = (int64_t)bs * kv_heads * parts * G * (kMfmaDim + 2) * (int64_t)sizeof(float);
   const bool fused = sync && sync_bytes >= qq_quest_layer_step_sync_bytes(bs, kv_heads) &&
                      fused_shape(q_dtype, kv_dtype, k_new ? new_dtype : -1, num_q_heads, kv_heads, head_dim,
@@ -686,7 +733,7 @@ static int forward_decode(
     a.bs = bs;
     a.G = G;
     const int blocks = bs * kStepKV * parts;
-    constexpr int kT = 64 * kHeadWaves;
+    constexpr int kT = 64 * kW4Waves;
     const int n_max = max(max_pages, k_sel);
     if (n_max <= 2 * kT)
       launch_attend_select<2>(a, blocks, s);
@@ -696,8 +743,12 @@ static int forward_decode(
       launch_attend_select<6>(a, blocks, s);
     else if (n_max <= 8 * kT)
       launch_attend_select<8>(a, blocks, s);
-    else
+    else if (n_max <= 12 * kT)
       launch_attend_select<12>(a, blocks, s);
+    else if (n_max <= 16 * kT)
+      launch_attend_select<16>(a, blocks, s);
+    else
+      launch_attend_select<24>(a, blocks, s);
     return check_launch(what);
   }
 
