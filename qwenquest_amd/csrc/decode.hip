@@ -743,6 +743,8 @@ static int forward_decode(
       launch_attend_select<6>(a, blocks, s);
     else if (n_max <= 8 * kT)
       launch_attend_select<8>(a, blocks, s);
+    else if (n_max <= 9 * kT)  // contexts just past 128K tokens
+      launch_attend_select<9>(a, blocks, s);
     else if (n_max <= 12 * kT)
       launch_attend_select<12>(a, blocks, s);
     else if (n_max <= 16 * kT)
