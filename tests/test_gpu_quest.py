@@ -525,18 +525,20 @@ def test_forward_decode_fused_path_engine_flow(flow):
 R2T_LAYOUTS = ("page_runs", "scattered", "mixed")
 
 
-@pytest.mark.parametrize("layout", R2T_LAYOUTS)
-def test_fused_step_req_to_token_layouts(layout):
+@pytest.mark.parametrize("layout,ctx", [(lay, 3200) for lay in R2T_LAYOUTS] +
+                         [("page_runs", 147456), ("scattered", 196608)])
+def test_fused_step_req_to_token_layouts(layout, ctx):
     """The fused layer step over req_to_token layouts that are not one run per request:
     pages as runs at shuffled bases, scattered rows, and page runs broken by swapped rows.
     Positions bit-exact vs the oracle, outputs within 2e-2 of the oracle's attention over
-    r2t[req, positions]."""
+    r2t[req, positions].  The long tables (2304 and 3072 pages) take the selection's 9- and
+    12-keys-per-thread forms."""
     from qwenquest_amd.attention.quest_only import QuestOnlyBackend
     from qwenquest_amd.batch import ForwardBatch, ForwardMode
     from qwenquest_amd.memory import MHATokenToKVPool, ReqToTokenPool
 
-    H, KV, D, P, TOP_K, CTX = 32, 4, 128, 64, 1024, 3200
-    prompt = {0: 3000, 1: 1500, 2: 2100}
+    H, KV, D, P, TOP_K, CTX = 32, 4, 128, 64, 1024, ctx
+    prompt = {0: CTX - 200, 1: CTX * 15 // 32, 2: CTX * 21 // 32}
     steps = 4
     nreq = len(prompt)
     rows_total = nreq * CTX + 1
