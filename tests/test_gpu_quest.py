@@ -451,6 +451,7 @@ ENGINE_FLOWS = [
     (1, 16, 4, 128, 16, 48, 600, {0: 500, 1: 40, 2: 47}, 12),
     (1, 4, 4, 128, 8, 64, 700, {0: 650, 2: 63}, 6),
     (1, 64, 8, 128, 32, 256, 1500, {0: 1400, 1: 255}, 4),
+    (1, 64, 4, 128, 64, 2048, 6000, {0: 5900, 1: 2100, 2: 300}, 3),  # 16 q heads per KV head, fused
 ]
 
 
