@@ -213,6 +213,32 @@ int qq_quest_forward_decode(const void* q, int q_dtype, int64_t q_batch_stride, 
                             float* scores_ws, int32_t* positions, void* out, void* workspace,
                             int64_t workspace_bytes, void* sync, int64_t sync_bytes, void* stream);
 
+/* qq_quest_forward_decode without caller workspaces: the page scores, the
+ * attention partials and the hand-off counters live in one fixed device array
+ * of qq_quest_forward_decode_noalloc_max_bytes() bytes (16 MiB: 64 KiB of
+ * counters, 4 MiB - 64 KiB of scores, 12 MiB of partials) that each GPU holds
+ * until the process ends.  No counterpart in the reference: it is for callers
+ * that cannot allocate device memory (code under graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  The call allocates nothing; the
+ * first call on a device looks the array up and clears its counters on
+ * `stream`.  Sizes beyond the array (bs * max_pages * 4 B of scores, the
+ * qq_decode_attention_workspace_bytes(bs, top_k, H, D) of partials) return
+ * QQ_EINVAL.  Every call on a device shares its array: calls that overlap on
+ * one GPU (two streams, two threads) race.  Arguments and results otherwise
+ * as qq_quest_forward_decode (same kernels, bit-identical outputs). */
+int qq_quest_forward_decode_noalloc(const void* q, int q_dtype, int64_t q_batch_stride, int num_q_heads,
+                                    const void* k_new, const void* v_new, int new_dtype,
+                                    const int64_t* out_cache_loc, void* k_layer, void* v_layer,
+                                    int kv_dtype, int64_t kv_rows, const uint16_t* page_k_bounds,
+                                    int layer, const int64_t* req_pool_indices, const int64_t* seq_lens,
+                                    const int32_t* candidate_limit, const int32_t* actual_lens, int bs,
+                                    int max_reqs, int max_pages, int kv_heads, int head_dim,
+                                    int page_size, int top_k, const int32_t* req_to_token,
+                                    int64_t req_to_token_stride, int64_t req_to_token_rows, float scale,
+                                    int32_t* positions, void* out, void* stream);
+/* Bytes of qq_quest_forward_decode_noalloc's per-device scratch array. */
+int64_t qq_quest_forward_decode_noalloc_max_bytes(void);
+
 /* qq_quest_forward_decode split into its two stages, for callers that run
  * other work between them or time them separately: phase 1 = page scoring and
  * the new token's K/V store, phase 2 = selection + layout + attention

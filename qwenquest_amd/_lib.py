@@ -65,6 +65,12 @@ SIGNATURES: dict[str, tuple] = {
         [_P, _I, _L, _I, _P, _P, _I, _P, _P, _P, _I, _L, _P, _I, _P, _P, _P, _P, _I, _I, _I, _I,
          _I, _I, _I, _P, _L, _L, _F, _P, _P, _P, _P, _L, _P, _L, _I, _P],
     ),
+    "qq_quest_forward_decode_noalloc": (
+        _I,
+        [_P, _I, _L, _I, _P, _P, _I, _P, _P, _P, _I, _L, _P, _I, _P, _P, _P, _P, _I, _I, _I, _I,
+         _I, _I, _I, _P, _L, _L, _F, _P, _P, _P],
+    ),
+    "qq_quest_forward_decode_noalloc_max_bytes": (_L, []),
     "qq_quest_layer_step_sync_bytes": (_L, [_I, _I]),
     "qq_dense_forward_decode": (
         _I,

@@ -29,6 +29,7 @@
 // output: score (all CUs) -> select + new-token store (one block per request)
 // -> chunk attention (MFMA) -> merge.
 #include <algorithm>
+#include <mutex>
 
 #include "qq_quest_dev.h"
 
@@ -810,4 +811,86 @@ extern "C" int qq_quest_forward_decode_phase(
       kv_dtype, kv_rows, page_k_bounds, layer, req_pool_indices, seq_lens, candidate_limit, actual_lens, bs,
       max_reqs, max_pages, kv_heads, head_dim, page_size, top_k, req_to_token, req_to_token_stride,
       req_to_token_rows, scale, scores_ws, positions, out, workspace, workspace_bytes, sync, sync_bytes, phase, static_cast<hipStream_t>(stream), "qq_quest_forward_decode_phase");
+}
+
+// ------------------------------------------------------------ no allocation
+// qq_quest_forward_decode_noalloc: the same layer with its scratch (page
+// scores, attention partials, hand-off counters) in one file-scope device
+// array instead of caller workspaces, for callers that cannot allocate.  Each
+// device holds its own copy; its address is looked up once per device and the
+// counter region is cleared there, after which every call leaves it cleared.
+namespace {
+
+constexpr int64_t kScratchBytes = 16ll << 20;
+constexpr int64_t kScratchSyncBytes = 64ll << 10;             // [0, 64 KiB): counters
+constexpr int64_t kScratchScoreBytes = (4ll << 20) - kScratchSyncBytes;  // [64 KiB, 4 MiB): page scores
+constexpr int64_t kScratchWorkOffset = 4ll << 20;              // [4 MiB, 16 MiB): attention partials
+constexpr int64_t kScratchWorkBytes = kScratchBytes - kScratchWorkOffset;
+
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+unsigned char* g_scratch_ptr[kMaxDevices] = {nullptr};
+
+__global__ void zero_words_kernel(uint32_t* p, int64_t n) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = 0u;
+}
+
+// The current device's scratch address (looked up, and its counters cleared
+// on `s`, on the first call on that device); nullptr with the error recorded.
+unsigned char* device_scratch(hipStream_t s) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    set_error(QQ_EHIP, "qq_quest_forward_decode_noalloc: no current HIP device (or device id >= %d)", kMaxDevices);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev]) return g_scratch_ptr[dev];
+  void* p = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || !p) {
+    set_error(QQ_EHIP, "qq_quest_forward_decode_noalloc: hipGetSymbolAddress(scratch) failed: %s",
+              hipGetErrorString(e));
+    return nullptr;
+  }
+  zero_words_kernel<<<64, 256, 0, s>>>(static_cast<uint32_t*>(p), kScratchSyncBytes / 4);
+  if (check_launch("qq_quest_forward_decode_noalloc (scratch clear)") != QQ_OK) return nullptr;
+  g_scratch_ptr[dev] = static_cast<unsigned char*>(p);
+  return g_scratch_ptr[dev];
+}
+
+}  // namespace
+
+extern "C" int64_t qq_quest_forward_decode_noalloc_max_bytes(void) { return kScratchBytes; }
+
+extern "C" int qq_quest_forward_decode_noalloc(
+    const void* q, int q_dtype, int64_t q_batch_stride, int num_q_heads, const void* k_new,
+    const void* v_new, int new_dtype, const int64_t* out_cache_loc, void* k_layer, void* v_layer,
+    int kv_dtype, int64_t kv_rows, const uint16_t* page_k_bounds, int layer,
+    const int64_t* req_pool_indices, const int64_t* seq_lens, const int32_t* candidate_limit,
+    const int32_t* actual_lens, int bs, int max_reqs, int max_pages, int kv_heads, int head_dim,
+    int page_size, int top_k, const int32_t* req_to_token, int64_t req_to_token_stride,
+    int64_t req_to_token_rows, float scale, int32_t* positions, void* out, void* stream) {
+  const char* what = "qq_quest_forward_decode_noalloc";
+  QQ_REQUIRE(bs >= 0 && max_pages > 0 && kv_heads > 0 && head_dim > 0 && num_q_heads > 0, "%s: bad sizes", what);
+  if (bs == 0) return QQ_OK;
+  const int64_t sync_need = qq_quest_layer_step_sync_bytes(bs, kv_heads);
+  const int64_t score_need = (int64_t)bs * max_pages * (int64_t)sizeof(float);
+  const int64_t work_need = qq_decode_attention_workspace_bytes(bs, top_k, num_q_heads, head_dim);
+  QQ_REQUIRE(sync_need <= kScratchSyncBytes && score_need <= kScratchScoreBytes && work_need <= kScratchWorkBytes,
+             "%s: batch %d x %d pages x top_k %d needs %lld B of counters, %lld B of scores and %lld B of "
+             "partials; the fixed scratch holds %lld, %lld and %lld",
+             what, bs, max_pages, top_k, (long long)sync_need, (long long)score_need, (long long)work_need,
+             (long long)kScratchSyncBytes, (long long)kScratchScoreBytes, (long long)kScratchWorkBytes);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  unsigned char* base = device_scratch(s);
+  if (!base) return QQ_EHIP;
+  return forward_decode(q, q_dtype, q_batch_stride, num_q_heads, k_new, v_new, new_dtype, out_cache_loc, k_layer,
+                        v_layer, kv_dtype, kv_rows, page_k_bounds, layer, req_pool_indices, seq_lens, candidate_limit,
+                        actual_lens, bs, max_reqs, max_pages, kv_heads, head_dim, page_size, top_k, req_to_token,
+                        req_to_token_stride, req_to_token_rows, scale,
+                        reinterpret_cast<float*>(base + kScratchSyncBytes), positions, out, base + kScratchWorkOffset,
+                        kScratchWorkBytes, base, kScratchSyncBytes, 3, s, what);
 }
