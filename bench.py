@@ -45,16 +45,37 @@ HBM_PEAK_GBS = 8000.0
 PROFILE = os.path.join(ROOT, "profiles", "quest_layer_step_kernels_b16_128k.md")
 
 
-def profiled_traffic() -> dict:
-    """HBM bytes per launch of each layer-step kernel, from the committed rocprofv3 PMC
-    summary (FETCH_SIZE + WRITE_SIZE, copy-calibrated); {} when the summary is absent."""
+def sources_sha16() -> str:
+    """Hash of the HIP sources the library is built from (qwenquest_amd/csrc)."""
+    import glob
+    import hashlib
+
+    h = hashlib.sha256()
+    for f in sorted(glob.glob(os.path.join(ROOT, "qwenquest_amd", "csrc", "*"))):
+        if f.endswith((".hip", ".h")):
+            h.update(os.path.basename(f).encode())
+            h.update(open(f, "rb").read())
+    return h.hexdigest()[:16]
+
+
+def profiled_traffic() -> tuple[dict, dict]:
+    """HBM bytes per launch of each layer-step kernel from the committed rocprofv3 PMC summary
+    (FETCH_SIZE + WRITE_SIZE, copy-calibrated), and its provenance: the summary records the
+    hash of the sources it was measured on, and the figures are used only when it matches the
+    sources of this build ({} otherwise: a stale profile prints no traffic)."""
+    traffic, recorded = {}, None
     try:
         for line in open(PROFILE):
             if line.startswith("traffic_bytes_per_launch:"):
-                return {k: int(v) for k, v in (kv.split("=") for kv in line.split(":", 1)[1].split())}
+                traffic = {k: int(v) for k, v in (kv.split("=") for kv in line.split(":", 1)[1].split())}
+            elif line.startswith("sources_sha16:"):
+                recorded = line.split(":", 1)[1].strip()
     except OSError:
         pass
-    return {}
+    current = sources_sha16()
+    source = {"file": os.path.relpath(PROFILE, ROOT), "sources_sha16": recorded, "build_sources_sha16": current,
+              "sources_match": recorded == current}
+    return (traffic if recorded == current else {}), source
 
 
 class Layer:
@@ -88,38 +109,45 @@ def time_graph(fn, reps: int, stream) -> float:
     return start.elapsed_time(end) / (3 * reps)
 
 
-def cpu_baseline(top_k, page, heads, kv, dim, ctx, sample_reqs: int, seconds: float) -> dict:
-    """The oracle (numpy, BLAS held to one thread) on one layer of `sample_reqs` generated
-    requests at full context, evaluated over and over (a fresh query each time) for about
-    `seconds` of CPU time; the median time per request-layer."""
-    from threadpoolctl import threadpool_limits
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
-    from oracle import attention as oa
-    from oracle import bf16
-    from oracle import quest as oq
 
-    rng = np.random.default_rng(7)
-    n_pages = ctx // page
-    reqs = []
-    for _ in range(sample_reqs):
-        bounds = bf16.from_f32(np.sort(rng.standard_normal((n_pages, kv, dim, 2), dtype=np.float32), axis=-1))
-        k = bf16.round_f32(rng.standard_normal((ctx, kv, dim), dtype=np.float32))
-        v = bf16.round_f32(rng.standard_normal((ctx, kv, dim), dtype=np.float32))
-        reqs.append((bounds, k, v))
+def cpu_baseline(be, q, batch, top_k: int, page: int, scaling: float, reps: int = 20, warmup: int = 3) -> dict:
+    """The reference's op sequence on the host cores (oracle/torch_path.py: group_queries ->
+    page_scores -> masked topk -> req_to_token gather -> fp32 decode_attention, torch CPU
+    kernels), on the same tensors the GPU holds for layer 0 (copied to host memory), with
+    every core of this process's CPU set; the median of `reps` timed layer-steps after
+    `warmup` untimed ones.  Also reports whether its positions equal the GPU's for that
+    layer (torch.topk's tie order aside, they must)."""
+    from oracle import torch_path as tp
+
+    threads = max(1, min(len(os.sched_getaffinity(0)), int(os.environ.get("OMP_NUM_THREADS", "0")) or 1 << 30))
+    torch.set_num_threads(threads)
+    quest = be.quest
+    pool = be.token_to_kv_pool
+    bounds = quest.page_k_bounds[0].cpu()
+    k_buf, v_buf = pool.k_all[0].cpu(), pool.v_all[0].cpu()
+    r2t = be.req_to_token.cpu()
+    qc = q.cpu()
+    rpi = batch.req_pool_indices.cpu()
+    seq = batch.seq_lens.cpu()
     times = []
-    with threadpool_limits(limits=1):
-        t_end = time.perf_counter() + seconds
-        while len(times) < 3 or time.perf_counter() < t_end:
-            bounds, k, v = reqs[len(times) % sample_reqs]
-            q = bf16.round_f32(rng.standard_normal((1, heads, dim), dtype=np.float32))
-            t0 = time.perf_counter()
-            qbar = oq.group_queries(q, kv, dim, is_bf16=True)
-            lay = oq.step_layout([ctx], page, top_k, False)
-            pos, actual, _ = oq.retrieve_topk(qbar, bounds[None], lay, page, top_k)
-            oa.sparse_decode(q, k, v, [pos[0, : int(actual[0])]], dim**-0.5)
+    for i in range(warmup + reps):
+        t0 = time.perf_counter()
+        pos, actual, _ = tp.layer_step(qc, bounds, rpi, seq, r2t, k_buf, v_buf, page, top_k, scaling)
+        if i >= warmup:
             times.append(time.perf_counter() - t0)
-    return {"per_request_s": float(np.median(times)), "reqs": sample_reqs, "evaluations": len(times),
-            "cpu_s": float(np.sum(times))}
+    gpu_pos = be._positions[: qc.shape[0]].cpu()
+    same = all(torch.equal(pos[i, : int(actual[i])], gpu_pos[i, : int(actual[i])]) for i in range(qc.shape[0]))
+    return {"us": float(np.median(times)) * 1e6, "threads": threads, "reps": reps, "warmup": warmup,
+            "positions_equal_gpu": bool(same)}
 
 
 def pinned_h2d_peak(nbytes: int = 1 << 30, reps: int = 5) -> float:
@@ -319,8 +347,7 @@ def main() -> int:
     ap.add_argument("--ctx", type=int, default=131072)
     ap.add_argument("--layers", type=int, default=48)
     ap.add_argument("--no-graph", action="store_true")
-    ap.add_argument("--cpu-sample", type=int, default=2, help="requests in the CPU-baseline sample (0 = skip)")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU time the baseline sample runs for")
+    ap.add_argument("--cpu-reps", type=int, default=20, help="timed CPU-baseline layer-steps (0 = skip)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB three times (scale for the HBM byte counters)")
     ap.add_argument("--ragged", action="store_true",
@@ -452,15 +479,21 @@ def main() -> int:
         "score_pages_fast_kernel", ms_sel, byts["bounds"], bw_sel)
 
     cpu = None
-    if args.cpu_sample > 0 and not args.ragged:
-        cores = 1
-        c = cpu_baseline(TOP_K, P, H, KV, D, S, args.cpu_sample, args.cpu_seconds)
-        us_cpu = c["per_request_s"] * B * 1e6
-        cpu = {"value": round(us_cpu, 1), "unit": "us per layer-step", "cores": cores, "kind": "port",
-               "sample": f"numpy oracle (one thread), {c['evaluations']} request-layer evaluations "
-                         f"({c['cpu_s']:.1f} s) over {args.cpu_sample} generated requests at {S} tokens "
-                         f"(GQA mean + scores + top-k + gather + attention); median per request x {B}"}
+    if args.cpu_reps > 0:
+        # the GPU's own state for layer 0 after the timed steps: run that layer once more so
+        # its positions are in the backend's buffer, then the same layer-step on the host
+        be.quest.prepare_step(seq_lens)
+        be.forward_decode(q_all[0], k_new[0], v_new[0], layers[0], batch)
+        torch.cuda.synchronize()
+        c = cpu_baseline(be, q_all[0], batch, TOP_K, P, D**-0.5, reps=args.cpu_reps)
+        cpu = {"value": round(c["us"], 1), "unit": "us per layer-step", "cores": c["threads"], "kind": "port",
+               "cpu_model": cpu_model(), "positions_equal_gpu": c["positions_equal_gpu"],
+               "sample": f"one whole layer-step (all {B} requests, layer 0 of the GPU's state: its bounds, "
+                         f"queries, req_to_token and K/V pool copied to host memory), torch CPU restatement "
+                         f"of the reference op sequence (scores -> masked top-k -> gather -> fp32 attention), "
+                         f"{c['threads']} threads, median of {c['reps']} after {c['warmup']} warm-ups"}
 
+    traffic, traffic_source = profiled_traffic()
     ctx_desc = (f"contexts uniform in [8192, {S}] (seeded, mean {int(ctxs.mean())})" if args.ragged
                 else f"{S}-token context")
     line = {
@@ -487,7 +520,8 @@ def main() -> int:
                        "quest_attend_w4_kernel": round(ms_att * 1e3, 2)},
         "roofline": {"kernel": dominant[0], "bound": "hbm", "achieved": round(dominant[3], 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(dominant[3] / HBM_PEAK_GBS, 4),
-                     "traffic": None if args.ragged else profiled_traffic().get(dominant[0])},
+                     "traffic": None if args.ragged else traffic.get(dominant[0]),
+                     "traffic_source": traffic_source},
         "cpu_baseline": cpu,
         "setup_s": round(setup_s, 1),
     }

@@ -305,7 +305,11 @@ int qq_kv_scatter(void* k_layer, void* v_layer, int buf_dtype, int64_t kv_rows, 
  * does, stats[0..2] += (hits, misses, fast-path calls).  copy_dst/copy_src
  * [bs, top_k] int64 and copy_count [bs] int32 are workspaces.  Too few victims
  * (coordinator.py:278-279) sets bit 1 of *error_flags, a missing host row
- * (:285-286) bit 2; that request is then left unchanged. */
+ * (:285-286) bit 2; that request's state is then left unchanged and its rows
+ * are all -1 (the rows attention then outputs NaN for it).  error_mirror (a
+ * device-accessible pointer to 3 int32 in pinned host memory, or NULL) gets
+ * word 0 / word 1 set to 1 with the same conditions, so the host can poll for
+ * errors without a device synchronisation. */
 int qq_hisparse_swap_in(const int32_t* positions, int64_t positions_stride,
                         const int32_t* actual_lens, const int64_t* seq_lens,
                         const int64_t* req_pool_indices, int bs, int max_reqs,
@@ -315,7 +319,7 @@ int qq_hisparse_swap_in(const int32_t* positions, int64_t positions_stride,
                         const void* host_k_layer, const void* host_v_layer, int64_t row_bytes,
                         int64_t host_rows, int64_t* rows_out, int64_t* copy_dst,
                         int64_t* copy_src, int32_t* copy_count, uint64_t* stats,
-                        int32_t* error_flags, void* stream);
+                        int32_t* error_flags, int32_t* error_mirror, void* stream);
 
 /* Row copies over n_layers layers: dst[layer][dst_idx[i]] = src[layer][src_idx[i]]
  * (row_bytes each; indices outside [0, rows) are skipped).  Carries the
@@ -335,13 +339,36 @@ int qq_hisparse_request_state(int64_t* buffer_tokens, int64_t* lru_slots, int nu
                               int64_t max_context_len, int req, const int64_t* host_idx, int64_t n,
                               int release, void* stream);
 
-/* Eager-backup bookkeeping (coordinator.py:201-212): for listed request i with
- * previous position seq_lens[i]-2, device_rows[i] = req*(buf+1) + min(seq-2, buf)
- * and req_to_host_pool[req, seq-2] = host_idx[i]. */
-int qq_hisparse_backup_index(const int64_t* req_indices, const int64_t* seq_lens,
-                             const int64_t* host_idx, int n, int device_buffer_size, int max_reqs,
-                             int64_t* req_to_host_pool, int64_t max_context_len,
-                             int64_t* device_rows, void* stream);
+/* Replaces the eager backup's bookkeeping of HiSparseCoordinator.prepare_decode_step
+ * (coordinator.py:183-212) without host synchronisation: batch entry b (request
+ * req_pool_indices[b], previous position seq_lens[b]-2) is skipped, and its
+ * request's skip flag cleared, when skip_flags[req] is set (the first decode step
+ * after admission, coordinator.py:193-195); otherwise it takes the next free host
+ * row in batch order from the device free list (free_ring / free_state, see
+ * qq_hisparse_ring_alloc), req_to_host_pool[req, seq-2] = that row,
+ * host_idx[b] = that row and device_rows[b] = req*(buf+1) + min(seq-2, buf) (the
+ * previous token's hot-buffer row); skipped entries get -1 in both.  Fewer free
+ * rows than entries (TokenToKVPoolAllocator.alloc's error, memory.py:62-66):
+ * bit 4 of *error_flags (and error_mirror word 2), nothing taken. */
+int qq_hisparse_backup_step(const int64_t* req_pool_indices, const int64_t* seq_lens, int bs,
+                            uint8_t* skip_flags, int device_buffer_size, int max_reqs,
+                            int64_t* req_to_host_pool, int64_t max_context_len, const int64_t* free_ring,
+                            int64_t* free_state, int64_t free_cap, int64_t* host_idx, int64_t* device_rows,
+                            int32_t* error_flags, int32_t* error_mirror, void* stream);
+
+/* The host tier's TokenToKVPoolAllocator (memory.py:47-70) kept on the device so that
+ * a decode step needs no host synchronisation: free_ring [free_cap] int64 with
+ * free_state = {head, count} int64 holds the free rows in order,
+ * free_ring[(head + i) % free_cap] for i < count.  alloc(n): out[i] = the i-th free
+ * row (fewer than n free: bit 4 of *error_flags, error_mirror word 2, out = -1,
+ * nothing taken). */
+int qq_hisparse_ring_alloc(const int64_t* free_ring, int64_t* free_state, int64_t free_cap, int64_t n,
+                           int64_t* out, int32_t* error_flags, int32_t* error_mirror, void* stream);
+
+/* free(rows): the entries rows[i] > 0 are appended at the tail in order
+ * (TokenToKVPoolAllocator.free, memory.py:68-72). */
+int qq_hisparse_ring_free(int64_t* free_ring, int64_t* free_state, int64_t free_cap, const int64_t* rows,
+                          int64_t n, void* stream);
 
 /* Replaces HiSparseCoordinator.write_new_token (coordinator.py:217-228): the new
  * K/V of request i goes to hot-buffer slot min(seq_lens[i]-1, buf). */

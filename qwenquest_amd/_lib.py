@@ -82,11 +82,13 @@ SIGNATURES: dict[str, tuple] = {
     "qq_hisparse_swap_in": (
         _I,
         [_P, _L, _P, _P, _P, _I, _I, _I, _I, _P, _P, _P, _L, _P, _P, _P, _P, _L, _L, _P, _P, _P,
-         _P, _P, _P, _P],
+         _P, _P, _P, _P, _P],
     ),
     "qq_copy_rows": (_I, [_P, _L, _L, _P, _P, _L, _L, _P, _I, _I, _L, _P]),
     "qq_hisparse_request_state": (_I, [_P, _P, _I, _I, _I, _P, _L, _I, _P, _L, _I, _P]),
-    "qq_hisparse_backup_index": (_I, [_P, _P, _P, _I, _I, _I, _P, _L, _P, _P]),
+    "qq_hisparse_backup_step": (_I, [_P, _P, _I, _P, _I, _I, _P, _L, _P, _P, _L, _P, _P, _P, _P, _P]),
+    "qq_hisparse_ring_alloc": (_I, [_P, _P, _L, _L, _P, _P, _P, _P]),
+    "qq_hisparse_ring_free": (_I, [_P, _P, _L, _P, _L, _P]),
     "qq_hisparse_write_new_token": (_I, [_P, _P, _I, _P, _P, _I, _P, _P, _I, _I, _I, _L, _P]),
     "qq_host_device_pointer": (_I, [_P, ctypes.POINTER(ctypes.c_void_p)]),
 }

@@ -47,10 +47,12 @@ __global__ __launch_bounds__(kThreads) void attn_chunk_kernel(AttnArgs a) {
   float* s_m = s_p + H * kChunk;
   float* s_l = s_m + H;
 
+  int bad = 0;  // given rows: a real slot without a row (a failed swap-in) poisons the output
   if (tid < cnt) {
     int64_t row;
     if (a.rows) {
       row = a.rows[(int64_t)b * a.pos_stride + r0 + tid];
+      bad = row < 0;
     } else {
       const int64_t p = a.positions[(int64_t)b * a.pos_stride + r0 + tid];
       const int64_t req = a.rpi[b];
@@ -61,7 +63,7 @@ __global__ __launch_bounds__(kThreads) void attn_chunk_kernel(AttnArgs a) {
   }
   for (int i = tid; i < H * D; i += kThreads)
     s_q[i] = load_as_float(a.q, (int64_t)b * a.q_bstride + i, a.q_dtype);
-  __syncthreads();
+  const bool poison = __syncthreads_or(bad) != 0;
 
   const int G = H / a.KV;
   const int64_t rowe = (int64_t)a.KV * D;
@@ -86,7 +88,7 @@ __global__ __launch_bounds__(kThreads) void attn_chunk_kernel(AttnArgs a) {
       l += e;
     }
     s_m[h] = m;
-    s_l[h] = l;
+    s_l[h] = poison ? __builtin_nanf("") : l;  // NaN survives every weight of the merge
   }
   __syncthreads();
   const int64_t part = (int64_t)b * a.max_chunks + c;
@@ -133,7 +135,9 @@ __global__ __launch_bounds__(64 * KV) void attn_mfma_kernel(AttnArgs a) {
   // row pointers per KV head (row base + head * 128 channels)
   __shared__ const uint16_t* s_kp[KV][kChunk];
   __shared__ const uint16_t* s_vp[KV][kChunk];
+  int bad = 0;  // given rows: a real slot without a row (a failed swap-in) poisons the output
   if (threadIdx.x < kChunk) {
+    if (a.rows && threadIdx.x < cnt) bad = a.rows[(int64_t)b * a.pos_stride + r0 + threadIdx.x] < 0;
     const int64_t row = threadIdx.x < cnt ? chunk_row(a, b, r0 + threadIdx.x) : 0;
 #pragma unroll
     for (int h = 0; h < KV; ++h) {
@@ -141,7 +145,7 @@ __global__ __launch_bounds__(64 * KV) void attn_mfma_kernel(AttnArgs a) {
       s_vp[h][threadIdx.x] = static_cast<const uint16_t*>(a.v) + row * kRow + h * kMfmaDim;
     }
   }
-  __syncthreads();
+  const bool poison = __syncthreads_or(bad) != 0;
   float mx, sum;
   float4_t o[8];
   const uint16_t* qh = static_cast<const uint16_t*>(a.q) + (int64_t)b * a.q_bstride + (int64_t)w * G * kMfmaDim;
@@ -160,7 +164,7 @@ __global__ __launch_bounds__(64 * KV) void attn_mfma_kernel(AttnArgs a) {
   if (hi == 0 && lo < G) {
     float* ml = a.ws_ml + (part * a.H + w * G + lo) * 2;
     ml[0] = mx * kLn2;
-    ml[1] = sum;
+    ml[1] = poison ? __builtin_nanf("") : sum;
   }
 }
 

@@ -228,6 +228,7 @@ __device__ inline void attend_item(const StepArgs& a, int bh, int part, unsigned
     __syncthreads();  // the list is in s_pages before the row table reuses the LDS
   }
   int32_t* pos_out = !ROWS && h == 0 && sa.positions ? sa.positions + (int64_t)b * top_k : nullptr;
+  bool bad_row = false;  // rows mode: a real slot without a row (a failed swap-in) poisons the output
   for (int i0 = 0; i0 < per_block; i0 += kThreads * 4) {
     int64_t pv[4];
     int64_t rv[4];
@@ -256,6 +257,7 @@ __device__ inline void attend_item(const StepArgs& a, int bh, int part, unsigned
       const int slot = slot_base + i;
       if (i < per_block) {
         const int64_t row = rv[u];
+        if (ROWS && slot < n && row < 0) bad_row = true;
         sm.rows[i] = (slot < n && row >= 0 && row < a.kv_rows) ? (int32_t)row : 0;
         if (pos_out && slot < top_k) pos_out[slot] = (int32_t)pv[u];
       }
@@ -277,7 +279,11 @@ __device__ inline void attend_item(const StepArgs& a, int bh, int part, unsigned
     }
   }
   // the row table is in LDS; the position stores and query loads stay in flight
-  lds_barrier();
+  bool poison = false;
+  if constexpr (ROWS)
+    poison = __syncthreads_or(bad_row ? 1 : 0) != 0;
+  else
+    lds_barrier();
   // this wave's rows: local [r0, r0 + per_wave), real up to slot n
   constexpr int kStep = 16 * T;
   const int r0 = wave * per_wave;
@@ -315,7 +321,7 @@ __device__ inline void attend_item(const StepArgs& a, int bh, int part, unsigned
   }
   if (hi == 0 && lo < G) {
     sm.m[wave][lo] = M;
-    sm.l[wave][lo] = L;
+    sm.l[wave][lo] = poison ? __builtin_nanf("") : L;  // NaN survives every weight of the merge
   }
   __syncthreads();
   uint16_t* outp = a.out + (int64_t)b * sa.H * kMfmaDim + (int64_t)h * G * kMfmaDim;
@@ -334,7 +340,7 @@ __device__ inline void attend_item(const StepArgs& a, int bh, int part, unsigned
       Os += wgt * sm.o[w][head][d];
     }
     if (parts == 1) {
-      outp[idx] = f2bf(Ls > 0.0f ? Os / Ls : 0.0f);
+      outp[idx] = f2bf(!(Ls <= 0.0f) ? Os / Ls : 0.0f);  // NaN (a poisoned part) stays NaN
     } else {
       st_agent(a.part_o + (part_idx * G + head) * kMfmaDim + d, Os);
       if (d == 0) {
@@ -421,7 +427,7 @@ __device__ inline void attend_item(const StepArgs& a, int bh, int part, unsigned
         }
       }
     }
-    const bool any = Ls > 0.0f;
+    const bool any = !(Ls <= 0.0f);  // NaN (a poisoned part) stays NaN
     const uint32_t lo2 = (uint32_t)f2bf(any ? Os.x / Ls : 0.0f) | ((uint32_t)f2bf(any ? Os.y / Ls : 0.0f) << 16);
     const uint32_t hi2 = (uint32_t)f2bf(any ? Os.z / Ls : 0.0f) | ((uint32_t)f2bf(any ? Os.w / Ls : 0.0f) << 16);
     *reinterpret_cast<uint2*>(outp + head * kMfmaDim + d4) = make_uint2(lo2, hi2);

@@ -24,7 +24,7 @@
 //   without host backup, :285-286) are detected before any state is written
 //   and reported through a device error word.  A second grid-wide kernel then
 //   copies the missed rows host -> device.
-#include "qq_common.h"
+#include "qq_quest_dev.h"
 
 namespace qq {
 namespace {
@@ -35,6 +35,7 @@ constexpr int kMaxPerThread = 8;  // buf <= 8192, top_k <= 8192 entries per thre
 constexpr int kEmpty = -1;
 constexpr int kErrVictims = 1;
 constexpr int kErrHostRow = 2;
+constexpr int kErrHostOom = 4;
 
 struct SwapArgs {
   const int32_t* positions;
@@ -54,6 +55,7 @@ struct SwapArgs {
   int32_t* copy_count;  // [bs]
   unsigned long long* stats;  // hits, misses, fast_path_calls
   int32_t* err;
+  int32_t* err_mirror;  // host-mapped words set to 1 per error kind (may be null)
   int table_size;  // power of two >= 2 * top_k
 };
 
@@ -121,32 +123,57 @@ __global__ __launch_bounds__(kPlanThreads) void swap_plan_kernel(SwapArgs a) {
   int* s_key = smem;                 // [T]
   int* s_val = s_key + T;            // [T] first entry index, later the slot
   int* s_vic = s_val + T;            // [top_k] victim slot of miss rank r
-  int* s_wave = s_vic + a.top_k;     // [kPlanWaves]
+  int* s_tok = s_vic + a.top_k;      // [buf] position cached by each slot (-1 none)
+  int* s_wave = s_tok + buf;         // [kPlanWaves]
   int* s_flag = s_wave + kPlanWaves; // [1] host-row error
   int64_t* tok = a.tokens + req * (int64_t)buf;
   int64_t* lru = a.lru + req * (int64_t)buf;
+  const int E = (buf + kPlanThreads - 1) / kPlanThreads;  // LRU entries per thread (a contiguous run)
+
+  // Every global load that does not depend on another goes out first: the entries'
+  // positions (i = tid + k*1024), the LRU order (j = tid*E + e) and every slot's token
+  // (t = tid + e*1024); the entries' host rows follow as soon as their positions are in.
+  int my_p[kMaxPerThread], my_slot[kMaxPerThread];
+  int64_t my_tok[kMaxPerThread], my_host[kMaxPerThread];
+#pragma unroll
+  for (int k = 0; k < kMaxPerThread; ++k) {
+    const int i = tid + k * kPlanThreads;
+    my_p[k] = i < n ? pos[i] : -1;
+    const int j = tid * E + k;
+    my_slot[k] = (k < E && j < buf) ? (int)lru[j] : -1;
+    const int t = tid + k * kPlanThreads;
+    my_tok[k] = t < buf ? tok[t] : -1;
+  }
+#pragma unroll
+  for (int k = 0; k < kMaxPerThread; ++k) {
+    const int64_t p = my_p[k];
+    my_host[k] = (p >= 0 && p < a.r2h_stride) ? a.r2h[req * a.r2h_stride + p] : -1;
+  }
   for (int h = tid; h < T; h += kPlanThreads) {
     s_key[h] = kEmpty;
     s_val[h] = 0x7FFFFFFF;
   }
   if (tid == 0) *s_flag = 0;
-  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < kMaxPerThread; ++k) {
+    const int t = tid + k * kPlanThreads;
+    if (t < buf) s_tok[t] = (my_tok[k] >= 0 && my_tok[k] < 0x7FFFFFFF) ? (int)my_tok[k] : -1;
+  }
+  lds_barrier();  // LDS-only: the host-row loads stay in flight
 
-  // entries i = tid + k*1024 (k < kMaxPerThread)
-  int my_p[kMaxPerThread], my_h[kMaxPerThread];
+  // dedup: insert every non-newest entry, keeping the smallest entry index (first occurrence)
+  int my_h[kMaxPerThread];
   bool my_new[kMaxPerThread];
   const int64_t newest_pos = s - 1;
 #pragma unroll
   for (int k = 0; k < kMaxPerThread; ++k) {
     const int i = tid + k * kPlanThreads;
-    my_p[k] = -1;
     my_h[k] = -1;
     my_new[k] = false;
     if (i < n) {
-      const int p = pos[i];
-      my_p[k] = p;
+      const int p = my_p[k];
       my_new[k] = (int64_t)p == newest_pos;
-      if (!my_new[k]) {  // insert, keep the smallest entry index (first occurrence)
+      if (!my_new[k]) {
         uint32_t h = slot_hash(p, mask);
         for (int probe = 0; probe <= mask; ++probe) {
           const int old = atomicCAS(&s_key[h], kEmpty, p);
@@ -160,40 +187,33 @@ __global__ __launch_bounds__(kPlanThreads) void swap_plan_kernel(SwapArgs a) {
       }
     }
   }
-  __syncthreads();
+  lds_barrier();
   bool my_first[kMaxPerThread];
 #pragma unroll
   for (int k = 0; k < kMaxPerThread; ++k) {
     const int i = tid + k * kPlanThreads;
     my_first[k] = i < n && !my_new[k] && my_h[k] >= 0 && s_val[my_h[k]] == i;
   }
-  __syncthreads();
+  lds_barrier();
   for (int h = tid; h < T; h += kPlanThreads) s_val[h] = -1;  // becomes position -> slot
-  __syncthreads();
+  lds_barrier();
 
-  // hits: LRU entries j = tid*E + e (contiguous runs, so ranks follow LRU order)
-  const int E = (buf + kPlanThreads - 1) / kPlanThreads;
-  int my_slot[kMaxPerThread];
+  // hits: the LRU run j = tid*E + e looks its slot's token up in the table
   bool my_hit[kMaxPerThread];
 #pragma unroll
   for (int e = 0; e < kMaxPerThread; ++e) {
-    const int j = tid * E + e;
-    my_slot[e] = -1;
     my_hit[e] = false;
-    if (e < E && j < buf) {
-      const int slot = (int)lru[j];
-      my_slot[e] = slot;
-      const int64_t t = (slot >= 0 && slot < buf) ? tok[slot] : -1;
-      if (t >= 0 && t < 0x7FFFFFFF) {
-        const int h = table_find(s_key, (int)t, mask);
-        if (h >= 0) {
-          s_val[h] = slot;
-          my_hit[e] = true;
-        }
+    const int slot = my_slot[e];
+    const int t = (slot >= 0 && slot < buf) ? s_tok[slot] : -1;
+    if (t >= 0) {
+      const int h = table_find(s_key, t, mask);
+      if (h >= 0) {
+        s_val[h] = slot;
+        my_hit[e] = true;
       }
     }
   }
-  __syncthreads();
+  lds_barrier();
 
   // misses: first occurrences without a hit, ranked in entry order (entry i = tid + k*1024
   // is not contiguous per thread, so rank by a scan per k-round; rounds past n hold none)
@@ -224,6 +244,7 @@ __global__ __launch_bounds__(kPlanThreads) void swap_plan_kernel(SwapArgs a) {
   if (num_miss > n_ev) {  // coordinator.py:278-279
     if (tid == 0) {
       atomicOr(a.err, kErrVictims);
+      if (a.err_mirror) a.err_mirror[0] = 1;
       a.copy_count[b] = 0;
     }
     for (int i = tid; i < a.top_k; i += kPlanThreads) rows[i] = -1;
@@ -239,7 +260,7 @@ __global__ __launch_bounds__(kPlanThreads) void swap_plan_kernel(SwapArgs a) {
       }
     }
   }
-  __syncthreads();
+  lds_barrier();
   // victims: host rows must exist (coordinator.py:284-286), then record the copies
   int64_t* cdst = a.copy_dst + (int64_t)b * a.top_k;
   int64_t* csrc = a.copy_src + (int64_t)b * a.top_k;
@@ -247,18 +268,18 @@ __global__ __launch_bounds__(kPlanThreads) void swap_plan_kernel(SwapArgs a) {
   for (int k = 0; k < kMaxPerThread; ++k) {
     if (miss_rank[k] >= 0) {
       const int slot = s_vic[miss_rank[k]];
-      const int64_t p = my_p[k];
-      const int64_t host = (p >= 0 && p < a.r2h_stride) ? a.r2h[req * a.r2h_stride + p] : -1;
+      const int64_t host = my_host[k];
       if (host < 0) atomicOr(s_flag, 1);
       s_val[my_h[k]] = slot;
       cdst[miss_rank[k]] = base_row + slot;
       csrc[miss_rank[k]] = host;
     }
   }
-  __syncthreads();
+  lds_barrier();
   if (*s_flag) {
     if (tid == 0) {
       atomicOr(a.err, kErrHostRow);
+      if (a.err_mirror) a.err_mirror[1] = 1;
       a.copy_count[b] = 0;
     }
     for (int i = tid; i < a.top_k; i += kPlanThreads) rows[i] = -1;
@@ -359,22 +380,158 @@ __global__ __launch_bounds__(256) void request_state_kernel(int64_t* tokens, int
   }
 }
 
-// Eager backup bookkeeping (coordinator.py:201-212): for listed request i (prev
-// position seq-2, skipped when the flag is set), the device row of the previous
-// token and req_to_host_pool[req, seq-2] = host_idx[i].
-__global__ __launch_bounds__(256) void backup_index_kernel(const int64_t* reqs, const int64_t* seq,
-                                                         const int64_t* host_idx, int n, int buf,
-                                                         int R, int64_t* r2h, int64_t r2h_stride,
-                                                         int64_t* dev_rows) {
-  for (int i = threadIdx.x; i < n; i += 256) {
-    const int64_t req = reqs[i];
-    const int64_t prev = seq[i] - 2;
-    if (req < 0 || req >= R || prev < 0 || prev >= r2h_stride) {
-      dev_rows[i] = -1;
-      continue;
+// The host tier's free list on the device (TokenToKVPoolAllocator semantics,
+// memory.py:47-70): ring[(head + i) % cap] for i < count are the free rows in
+// order; alloc takes from the head, free appends at the tail.  state = {head, count}.
+
+// alloc(n) for an admission: out[i] = the i-th free row; QQ_ERUNTIME-style error
+// bit 4 (nothing taken) when fewer than n are free.
+__global__ __launch_bounds__(256) void ring_alloc_kernel(const int64_t* ring, int64_t* state, int64_t cap,
+                                                       int64_t n, int64_t* out, int32_t* err,
+                                                       int32_t* err_mirror) {
+  const int64_t head = state[0], count = state[1];
+  __syncthreads();
+  if (n > count) {
+    if (threadIdx.x == 0) {
+      atomicOr(err, kErrHostOom);
+      if (err_mirror) err_mirror[2] = 1;
     }
-    dev_rows[i] = req * (int64_t)(buf + 1) + min(prev, (int64_t)buf);
-    r2h[req * r2h_stride + prev] = host_idx[i];
+    for (int64_t i = threadIdx.x; i < n; i += 256) out[i] = -1;
+    return;
+  }
+  for (int64_t i = threadIdx.x; i < n; i += 256) out[i] = ring[(head + i) % cap];
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    state[0] = (head + n) % cap;
+    state[1] = count - n;
+  }
+}
+
+// free(rows): rows[i] > 0 are appended at the tail in order (one block; block scan).
+__global__ __launch_bounds__(256) void ring_free_kernel(int64_t* ring, int64_t* state, int64_t cap,
+                                                      const int64_t* rows, int64_t n) {
+  __shared__ int s_wave[4];
+  __shared__ int64_t s_base;  // free rows so far: the next one goes to ring[(head + s_base) % cap]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if (tid == 0) s_base = state[1];
+  const int64_t head = state[0];
+  __syncthreads();
+  for (int64_t i0 = 0; i0 < n; i0 += 256) {
+    const int64_t i = i0 + tid;
+    const int64_t r = i < n ? rows[i] : 0;
+    const int keep = r > 0 ? 1 : 0;
+    int x = keep;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int y = __shfl_up(x, off, 64);
+      if (lane >= off) x += y;
+    }
+    if (lane == 63) s_wave[wave] = x;
+    __syncthreads();
+    int wbase = 0, tot = 0;
+    for (int w = 0; w < 4; ++w) {
+      wbase += w < wave ? s_wave[w] : 0;
+      tot += s_wave[w];
+    }
+    const int64_t base = s_base;
+    const int64_t at = base + wbase + x - 1;
+    if (keep && at < cap) ring[(head + at) % cap] = r;  // more rows than the pool holds: dropped
+    __syncthreads();
+    if (tid == 0) s_base = base + tot;
+    __syncthreads();
+  }
+  if (tid == 0) state[1] = min(s_base, cap);
+}
+
+// The eager backup of one decode step (coordinator.py:183-212) without the host: for
+// batch entry b (request rpi[b], previous position seq[b] - 2), skip and clear it when
+// its request's skip flag is set (first step after admission); otherwise take the next
+// free host row in batch order, record req_to_host_pool[req, seq - 2] and the device
+// row of the previous token.  host_idx[b] / dev_rows[b] are -1 for skipped entries (the
+// fold and the copies skip them).  Too few free rows: error bit 4, nothing taken.
+__global__ __launch_bounds__(256) void backup_step_kernel(const int64_t* rpi, const int64_t* seq, int bs,
+                                                        uint8_t* skip, int buf, int R, int64_t* r2h,
+                                                        int64_t r2h_stride, const int64_t* ring, int64_t* state,
+                                                        int64_t cap, int64_t* host_idx, int64_t* dev_rows,
+                                                        int32_t* err, int32_t* err_mirror) {
+  __shared__ int s_wave[4];
+  __shared__ int s_total;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t head = state[0], count = state[1];
+  // pass 1: which entries back up (the flags are read before any is cleared)
+  int total = 0;
+  for (int b0 = 0; b0 < bs; b0 += 256) {
+    const int b = b0 + tid;
+    int want = 0;
+    if (b < bs) {
+      const int64_t req = rpi[b];
+      const int64_t prev = seq[b] - 2;
+      want = req >= 0 && req < R && !skip[req] && prev >= 0 && prev < r2h_stride ? 1 : 0;
+    }
+    int x = want;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int y = __shfl_up(x, off, 64);
+      if (lane >= off) x += y;
+    }
+    if (lane == 63) s_wave[wave] = x;
+    __syncthreads();
+    for (int w = 0; w < 4; ++w) total += s_wave[w];
+    __syncthreads();
+  }
+  if (tid == 0) s_total = total;
+  __syncthreads();
+  const bool oom = (int64_t)s_total > count;
+  if (oom && tid == 0) {
+    atomicOr(err, kErrHostOom);
+    if (err_mirror) err_mirror[2] = 1;
+  }
+  // pass 2: ranks in batch order, rows, bookkeeping
+  int base = 0;
+  for (int b0 = 0; b0 < bs; b0 += 256) {
+    const int b = b0 + tid;
+    int want = 0;
+    int64_t req = -1, prev = -1;
+    if (b < bs) {
+      req = rpi[b];
+      prev = seq[b] - 2;
+      want = req >= 0 && req < R && !skip[req] && prev >= 0 && prev < r2h_stride ? 1 : 0;
+    }
+    int x = want;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int y = __shfl_up(x, off, 64);
+      if (lane >= off) x += y;
+    }
+    if (lane == 63) s_wave[wave] = x;
+    __syncthreads();
+    int wbase = 0, tot = 0;
+    for (int w = 0; w < 4; ++w) {
+      wbase += w < wave ? s_wave[w] : 0;
+      tot += s_wave[w];
+    }
+    if (b < bs) {
+      if (want && !oom) {
+        const int64_t h = ring[(head + base + wbase + x - 1) % cap];
+        host_idx[b] = h;
+        r2h[req * r2h_stride + prev] = h;
+        dev_rows[b] = req * (int64_t)(buf + 1) + min(prev, (int64_t)buf);
+      } else {
+        host_idx[b] = -1;
+        dev_rows[b] = -1;
+      }
+    }
+    base += tot;
+    __syncthreads();
+  }
+  // clear the skip flags of this batch's requests (after every read of them above)
+  for (int b = tid; b < bs; b += 256) {
+    const int64_t req = rpi[b];
+    if (req >= 0 && req < R) skip[req] = 0;
+  }
+  if (tid == 0 && !oom) {
+    state[0] = (head + s_total) % cap;
+    state[1] = count - s_total;
   }
 }
 
@@ -407,6 +564,21 @@ __global__ __launch_bounds__(256) void write_new_kernel(Dst* k_dst, Dst* v_dst, 
 
 using namespace qq;
 
+// The plan kernel's LDS above the 64 KiB default (large buffers): opted in once per device.
+static constexpr int kPlanMaxLds = 160 * 1024;
+static int plan_lds_opt_in() {
+  static bool opted[64] = {false};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return set_error(QQ_EHIP, "qq_hisparse_swap_in: no device");
+  if (!opted[dev]) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&swap_plan_kernel),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, kPlanMaxLds);
+    if (e != hipSuccess) return set_error(QQ_EHIP, "qq_hisparse_swap_in: LDS opt-in failed: %s", hipGetErrorString(e));
+    opted[dev] = true;
+  }
+  return QQ_OK;
+}
+
 extern "C" int qq_hisparse_swap_in(const int32_t* positions, int64_t positions_stride,
                                    const int32_t* actual_lens, const int64_t* seq_lens,
                                    const int64_t* req_pool_indices, int bs, int max_reqs,
@@ -417,7 +589,7 @@ extern "C" int qq_hisparse_swap_in(const int32_t* positions, int64_t positions_s
                                    const void* host_v_layer, int64_t row_bytes,
                                    int64_t host_rows, int64_t* rows_out, int64_t* copy_dst,
                                    int64_t* copy_src, int32_t* copy_count, uint64_t* stats,
-                                   int32_t* error_flags, void* stream) {
+                                   int32_t* error_flags, int32_t* error_mirror, void* stream) {
   const char* what = "qq_hisparse_swap_in";
   QQ_REQUIRE(bs >= 0 && max_reqs > 0 && device_buffer_size >= top_k && top_k > 0,
              "%s: bad sizes (buf %d, top_k %d)", what, device_buffer_size, top_k);
@@ -430,8 +602,10 @@ extern "C" int qq_hisparse_swap_in(const int32_t* positions, int64_t positions_s
   if (bs == 0) return QQ_OK;
   int T = 1;
   while (T < 2 * top_k) T <<= 1;
-  const size_t smem = (size_t)(2 * T + top_k + kPlanWaves + 1) * sizeof(int);
-  QQ_REQUIRE(smem <= 64 * 1024, "%s: top_k %d needs %zu bytes of LDS", what, top_k, smem);
+  const size_t smem = (size_t)(2 * T + top_k + device_buffer_size + kPlanWaves + 1) * sizeof(int);
+  QQ_REQUIRE(smem <= kPlanMaxLds, "%s: top_k %d with a %d-slot buffer needs %zu bytes of LDS (at most %d)", what,
+             top_k, device_buffer_size, smem, kPlanMaxLds);
+  if (smem > 64 * 1024 && plan_lds_opt_in() != QQ_OK) return QQ_EHIP;
   SwapArgs a;
   a.positions = positions;
   a.pos_stride = positions_stride;
@@ -452,6 +626,7 @@ extern "C" int qq_hisparse_swap_in(const int32_t* positions, int64_t positions_s
   a.copy_count = copy_count;
   a.stats = reinterpret_cast<unsigned long long*>(stats);
   a.err = error_flags;
+  a.err_mirror = error_mirror;
   a.table_size = T;
   hipStream_t s = static_cast<hipStream_t>(stream);
   swap_plan_kernel<<<bs, kPlanThreads, smem, s>>>(a);
@@ -493,17 +668,41 @@ extern "C" int qq_hisparse_request_state(int64_t* buffer_tokens, int64_t* lru_sl
   return check_launch("qq_hisparse_request_state");
 }
 
-extern "C" int qq_hisparse_backup_index(const int64_t* req_indices, const int64_t* seq_lens,
-                                        const int64_t* host_idx, int n, int device_buffer_size,
-                                        int max_reqs, int64_t* req_to_host_pool,
-                                        int64_t max_context_len, int64_t* device_rows,
-                                        void* stream) {
-  QQ_REQUIRE(n >= 0 && device_buffer_size > 0, "qq_hisparse_backup_index: bad arguments");
+extern "C" int qq_hisparse_backup_step(const int64_t* req_pool_indices, const int64_t* seq_lens, int bs,
+                                       uint8_t* skip_flags, int device_buffer_size, int max_reqs,
+                                       int64_t* req_to_host_pool, int64_t max_context_len, const int64_t* free_ring,
+                                       int64_t* free_state, int64_t free_cap, int64_t* host_idx,
+                                       int64_t* device_rows, int32_t* error_flags, int32_t* error_mirror,
+                                       void* stream) {
+  QQ_REQUIRE(bs >= 0 && device_buffer_size > 0 && max_reqs > 0 && free_cap > 0,
+             "qq_hisparse_backup_step: bad arguments");
+  if (bs == 0) return QQ_OK;
+  QQ_REQUIRE(req_pool_indices && seq_lens && skip_flags && req_to_host_pool && free_ring && free_state && host_idx &&
+                 device_rows && error_flags,
+             "qq_hisparse_backup_step: null pointer");
+  backup_step_kernel<<<1, 256, 0, static_cast<hipStream_t>(stream)>>>(
+      req_pool_indices, seq_lens, bs, skip_flags, device_buffer_size, max_reqs, req_to_host_pool, max_context_len,
+      free_ring, free_state, free_cap, host_idx, device_rows, error_flags, error_mirror);
+  return check_launch("qq_hisparse_backup_step");
+}
+
+extern "C" int qq_hisparse_ring_alloc(const int64_t* free_ring, int64_t* free_state, int64_t free_cap, int64_t n,
+                                      int64_t* out, int32_t* error_flags, int32_t* error_mirror, void* stream) {
+  QQ_REQUIRE(n >= 0 && free_cap > 0, "qq_hisparse_ring_alloc: bad sizes");
   if (n == 0) return QQ_OK;
-  backup_index_kernel<<<1, 256, 0, static_cast<hipStream_t>(stream)>>>(
-      req_indices, seq_lens, host_idx, n, device_buffer_size, max_reqs, req_to_host_pool,
-      max_context_len, device_rows);
-  return check_launch("qq_hisparse_backup_index");
+  QQ_REQUIRE(free_ring && free_state && out && error_flags, "qq_hisparse_ring_alloc: null pointer");
+  ring_alloc_kernel<<<1, 256, 0, static_cast<hipStream_t>(stream)>>>(free_ring, free_state, free_cap, n, out,
+                                                                     error_flags, error_mirror);
+  return check_launch("qq_hisparse_ring_alloc");
+}
+
+extern "C" int qq_hisparse_ring_free(int64_t* free_ring, int64_t* free_state, int64_t free_cap, const int64_t* rows,
+                                     int64_t n, void* stream) {
+  QQ_REQUIRE(n >= 0 && free_cap > 0, "qq_hisparse_ring_free: bad sizes");
+  if (n == 0) return QQ_OK;
+  QQ_REQUIRE(free_ring && free_state && rows, "qq_hisparse_ring_free: null pointer");
+  ring_free_kernel<<<1, 256, 0, static_cast<hipStream_t>(stream)>>>(free_ring, free_state, free_cap, rows, n);
+  return check_launch("qq_hisparse_ring_free");
 }
 
 extern "C" int qq_hisparse_write_new_token(void* device_k_layer, void* device_v_layer,

@@ -8,12 +8,17 @@ Two tiers, the reference's layout and bookkeeping:
 * device: per request ``device_buffer_size`` LRU slots + 1 reserved newest-token
   slot (``device_k/v[layer]``, ``buffer_tokens``, ``lru_slots``).
 
-All copies and the swap-in planning run in HIP kernels on the current stream;
-the kernels read/write the pinned host tier directly over PCIe, so a decode
-step needs no host synchronisation.  The two error conditions of the
-reference's swap-in (too few victims, a position without host backup) are
-raised by :meth:`check_errors`, which :meth:`prepare_decode_step`, ``stats``
-and (with ``sync_errors=True``) every swap-in call run.
+All copies, the swap-in planning and the eager backup's bookkeeping (skip flags,
+host-row allocation from a free list kept on the device) run in HIP kernels on the
+current stream; the kernels read and write the pinned host tier directly over
+PCIe, so a decode step needs no host synchronisation and can be captured in a
+HIP graph.  The reference's error conditions (too few victims, a position without
+host backup, an exhausted host pool) are detected on the device: the affected
+request's swap-in rows become -1, which makes its attention output NaN, and the
+kernels set a device error word plus a mirror of it in pinned host memory.
+:meth:`check_errors` raises what the reference raises; ``prepare_decode_step``
+runs it on the mirror (no synchronisation, so an error surfaces one step late),
+``stats`` and ``sync_errors=True`` (after every swap-in) on the device word.
 """
 
 from __future__ import annotations
@@ -24,12 +29,43 @@ from dataclasses import dataclass
 import torch
 
 from qwenquest_amd import _lib
-from qwenquest_amd.memory import MHATokenToKVPool, TokenToKVPoolAllocator, kv_pair_zeros
+from qwenquest_amd.memory import MHATokenToKVPool, kv_pair_zeros
 from qwenquest_amd.quest import QuestAlgorithm
 
-__all__ = ["HiSparseCoordinator", "SwapInStats"]
+__all__ = ["DeviceRowAllocator", "HiSparseCoordinator", "SwapInStats"]
 
-_ERR_VICTIMS, _ERR_HOST_ROW = 1, 2
+_ERR_VICTIMS, _ERR_HOST_ROW, _ERR_HOST_OOM = 1, 2, 4
+
+
+class DeviceRowAllocator:
+    """The host tier's free list (``TokenToKVPoolAllocator``, reference memory.py:47-72) kept on
+    the device: ``ring[(head + i) % size]`` for ``i < count`` are the free rows in order, alloc
+    takes from the head, free appends at the tail - the reference's order of rows.  The decode
+    step's backups allocate from it inside a kernel; ``alloc``/``free`` serve admission and
+    release, ``available_size`` reads the count (a synchronisation, for introspection)."""
+
+    def __init__(self, size: int, device: torch.device, err: torch.Tensor, err_mirror_dev: int):
+        self.size = size
+        self.device = device
+        self.ring = torch.arange(1, size + 1, dtype=torch.int64, device=device)
+        self.state = torch.tensor([0, size], dtype=torch.int64, device=device)  # head, count
+        self._err, self._err_mirror_dev = err, err_mirror_dev
+
+    def available_size(self) -> int:
+        return int(self.state[1].item())
+
+    def alloc(self, n: int) -> torch.Tensor:
+        if n > self.available_size():
+            raise RuntimeError(f"KV pool out of memory: need {n} token slots, {self.available_size()} free")
+        out = torch.empty(n, dtype=torch.int64, device=self.device)
+        _lib.call("qq_hisparse_ring_alloc", _lib.ptr(self.ring), _lib.ptr(self.state), self.size, n, _lib.ptr(out),
+                  _lib.ptr(self._err), self._err_mirror_dev, _lib.stream(self.device))
+        return out
+
+    def free(self, indices: torch.Tensor) -> None:
+        idx = indices.to(device=self.device, dtype=torch.int64).flatten().contiguous()
+        _lib.call("qq_hisparse_ring_free", _lib.ptr(self.ring), _lib.ptr(self.state), self.size, _lib.ptr(idx),
+                  int(idx.numel()), _lib.stream(self.device))
 
 
 @dataclass
@@ -86,8 +122,7 @@ class HiSparseCoordinator:
         self.row_elems = kv_heads * head_dim
         self.row_bytes = self.row_elems * torch.tensor([], dtype=dtype).element_size()
 
-        # ---- host tier (pinned), full history of every request
-        self.host_allocator = TokenToKVPoolAllocator(host_pool_size, device="cpu")
+        # ---- host tier (pinned), full history of every request (rows from host_allocator)
         hshape = (num_layers, host_pool_size + 1, kv_heads, head_dim)
         self.host_k_all = torch.zeros(hshape, dtype=dtype, pin_memory=True)
         self.host_v_all = torch.zeros(hshape, dtype=dtype, pin_memory=True)
@@ -108,14 +143,22 @@ class HiSparseCoordinator:
         self._lru_init = torch.arange(buf, dtype=torch.int64, device=self.device)
         self.lru_slots = self._lru_init.repeat(num_layers, max_reqs, 1)
 
-        self._skip_first_backup = [False] * max_reqs
-        # swap-in workspaces + device counters (hits, misses, fast path) + error word
+        # swap-in workspaces + device counters (hits, misses, fast path) + error word, and the
+        # error word's mirror in pinned host memory (read by the host without a synchronisation)
         self._rows = torch.empty((max_reqs, top_k), dtype=torch.int64, device=self.device)
         self._copy_dst = torch.empty((max_reqs, top_k), dtype=torch.int64, device=self.device)
         self._copy_src = torch.empty((max_reqs, top_k), dtype=torch.int64, device=self.device)
         self._copy_count = torch.zeros(max_reqs, dtype=torch.int32, device=self.device)
         self._stats = torch.zeros(3, dtype=torch.int64, device=self.device)
         self._err = torch.zeros(1, dtype=torch.int32, device=self.device)
+        self._err_host = torch.zeros(4, dtype=torch.int32, pin_memory=True)
+        self._err_host_dev = self._device_address(self._err_host)
+        # the eager backup's per-step state, on the device: first-step skip flags and the
+        # host-row free list; persistent step buffers (graph capture)
+        self._skip_first_backup = torch.zeros(max_reqs, dtype=torch.uint8, device=self.device)
+        self.host_allocator = DeviceRowAllocator(host_pool_size, self.device, self._err, self._err_host_dev)
+        self._step_host_idx = torch.empty(max_reqs, dtype=torch.int64, device=self.device)
+        self._step_dev_rows = torch.empty(max_reqs, dtype=torch.int64, device=self.device)
 
     @staticmethod
     def _device_address(t: torch.Tensor) -> int:
@@ -128,11 +171,21 @@ class HiSparseCoordinator:
 
     # -------------------------------------------------- errors / stats
 
-    def check_errors(self) -> None:
-        """Raise what the reference raises inside _swap_in_long (coordinator.py:278-279, 285-286)."""
-        err = int(self._err.item())
+    def check_errors(self, sync: bool = True) -> None:
+        """Raise what the reference raises (coordinator.py:278-279, 285-286; memory.py:62-66) for
+        an error the kernels detected.  ``sync``: read the device error word (a synchronisation);
+        otherwise its mirror in pinned host memory, which the kernels write as they detect an
+        error (visible to the host once that kernel has finished)."""
+        if sync:
+            err = int(self._err.item())
+        else:
+            m = self._err_host.tolist()
+            err = (_ERR_VICTIMS if m[0] else 0) | (_ERR_HOST_ROW if m[1] else 0) | (_ERR_HOST_OOM if m[2] else 0)
         if err:
             self._err.zero_()
+            self._err_host.zero_()
+            if err & _ERR_HOST_OOM:
+                raise RuntimeError("KV pool out of memory: the host tier has no free rows for the eager backup")
             if err & _ERR_VICTIMS:
                 raise RuntimeError("device_buffer_size too small for this top-k")
             raise AssertionError("positions without host backup were selected")
@@ -159,7 +212,7 @@ class HiSparseCoordinator:
         buf = self.device_buffer_size
         stream = _lib.stream(self.device)
         idx = prefill_indices.to(device=self.device, dtype=torch.int64).contiguous()
-        host_idx = self.host_allocator.alloc(n).to(self.device)
+        host_idx = self.host_allocator.alloc(n)
         pool = token_to_kv_pool
         _lib.call("qq_hisparse_request_state", _lib.ptr(self.buffer_tokens), _lib.ptr(self.lru_slots),
                   self.num_layers, self.max_reqs, buf, _lib.ptr(self.req_to_host_pool),
@@ -177,7 +230,7 @@ class HiSparseCoordinator:
                       dst_all.stride(0) * dst_all.element_size(), dst_all.shape[1], _lib.ptr(dev_rows),
                       n_dev, self.num_layers, self.row_bytes, stream)
         self.quest.update_prefill_representations_fused(req, pool.k_all, idx)
-        self._skip_first_backup[req] = True
+        self._skip_first_backup[req] = 1
 
     # -------------------------------------------------- [H2] per decode step
 
@@ -185,33 +238,35 @@ class HiSparseCoordinator:
         return (seq_lens.long() - 1).clamp(max=self.device_buffer_size)
 
     def prepare_decode_step(self, req_pool_indices: torch.Tensor, seq_lens: torch.Tensor) -> None:
-        """[H2] Fold the previous token into the bounds, back it up to host (coordinator.py:183-215)."""
+        """[H2] Fold the previous token into the bounds and back it up to host
+        (coordinator.py:183-215), all on the device: the first step after admission is skipped
+        per request by a device flag, host rows come from the device free list in batch order,
+        and the fold and the copies skip the entries left at -1."""
         if not self.sync_errors:
-            self.check_errors()
-        reqs = req_pool_indices.tolist()
-        keep = []
-        for i, r in enumerate(reqs):
-            if self._skip_first_backup[r]:
-                self._skip_first_backup[r] = False
-            else:
-                keep.append(i)
-        if not keep:
+            self.check_errors(sync=False)
+        bs = int(req_pool_indices.shape[0])
+        if bs == 0:
             return
+        if bs > self.max_reqs:
+            raise ValueError(f"batch {bs} exceeds max_reqs {self.max_reqs}")
         stream = _lib.stream(self.device)
-        sel = torch.tensor(keep, dtype=torch.int64, device=self.device)
-        breqs = req_pool_indices.to(device=self.device, dtype=torch.int64)[sel].contiguous()
-        bseq = seq_lens.to(device=self.device, dtype=torch.int64)[sel].contiguous()
-        host_idx = self.host_allocator.alloc(len(keep)).to(self.device)
-        dev_rows = torch.empty(len(keep), dtype=torch.int64, device=self.device)
-        _lib.call("qq_hisparse_backup_index", _lib.ptr(breqs), _lib.ptr(bseq), _lib.ptr(host_idx), len(keep),
-                  self.device_buffer_size, self.max_reqs, _lib.ptr(self.req_to_host_pool),
-                  self.max_context_len, _lib.ptr(dev_rows), stream)
-        self.quest.update_decode_representations_fused(breqs, self.device_k_all, dev_rows)
+        rpi = req_pool_indices.to(device=self.device, dtype=torch.int64).contiguous()
+        seq = seq_lens.to(device=self.device, dtype=torch.int64).contiguous()
+        host_idx = self._step_host_idx[:bs]
+        dev_rows = self._step_dev_rows[:bs]
+        ha = self.host_allocator
+        _lib.call("qq_hisparse_backup_step", _lib.ptr(rpi), _lib.ptr(seq), bs, _lib.ptr(self._skip_first_backup),
+                  self.device_buffer_size, self.max_reqs, _lib.ptr(self.req_to_host_pool), self.max_context_len,
+                  _lib.ptr(ha.ring), _lib.ptr(ha.state), ha.size, _lib.ptr(host_idx), _lib.ptr(dev_rows),
+                  _lib.ptr(self._err), self._err_host_dev, stream)
+        self.quest.update_decode_representations_fused(rpi, self.device_k_all, dev_rows)
         for src_all, host_base in ((self.device_k_all, self._host_k_dev), (self.device_v_all, self._host_v_dev)):
             _lib.call("qq_copy_rows", _lib.ptr(src_all), src_all.stride(0) * src_all.element_size(),
                       src_all.shape[1], _lib.ptr(dev_rows), host_base,
                       self.host_k_all.stride(0) * self.host_k_all.element_size(), self.host_k_all.shape[1],
-                      _lib.ptr(host_idx), len(keep), self.num_layers, self.row_bytes, stream)
+                      _lib.ptr(host_idx), bs, self.num_layers, self.row_bytes, stream)
+        if self.sync_errors:
+            self.check_errors()
 
     def write_new_token(self, layer_id: int, req_pool_indices: torch.Tensor, seq_lens: torch.Tensor,
                         k: torch.Tensor, v: torch.Tensor) -> None:
@@ -261,7 +316,7 @@ class HiSparseCoordinator:
             self._host_layer(self._host_k_dev, layer_id), self._host_layer(self._host_v_dev, layer_id),
             self.row_bytes, self.host_k_all.shape[1], _lib.ptr(rows), _lib.ptr(self._copy_dst),
             _lib.ptr(self._copy_src), _lib.ptr(self._copy_count), _lib.ptr(self._stats), _lib.ptr(self._err),
-            _lib.stream(self.device),
+            self._err_host_dev, _lib.stream(self.device),
         )
         if self.sync_errors:
             self.check_errors()
@@ -272,12 +327,11 @@ class HiSparseCoordinator:
     def request_finished(self, req_pool_idx: int) -> None:
         """[H4] Free the host rows, reset the request's state and bounds (coordinator.py:308-316)."""
         req = int(req_pool_idx)
-        host_idx = self.req_to_host_pool[req].cpu()
-        self.host_allocator.free(host_idx[host_idx >= 0])
+        self.host_allocator.free(self.req_to_host_pool[req])  # its rows >= 0, in position order
         _lib.call("qq_hisparse_request_state", _lib.ptr(self.buffer_tokens), _lib.ptr(self.lru_slots),
                   self.num_layers, self.max_reqs, self.device_buffer_size, _lib.ptr(self.req_to_host_pool),
                   self.max_context_len, req, None, 0, 1, _lib.stream(self.device))
-        self._skip_first_backup[req] = False
+        self._skip_first_backup[req] = 0
         self.quest.invalidate_request(req)
 
     # -------------------------------------------------- introspection

@@ -220,14 +220,23 @@ class QuestAlgorithm:
     def update_prefill_representations_fused(
         self, req_pool_idx: int, k_all: torch.Tensor, prefill_indices: torch.Tensor
     ) -> None:
-        """[Q2] All layers in one launch; ``k_all`` is ``[num_layers, rows, KV, D]``
-        (``MHATokenToKVPool.k_all``), layer ``i`` holding Quest layer ``start_layer + i``."""
-        if k_all.dim() != 4 or not k_all.is_contiguous():
-            raise ValueError("k_all must be a contiguous [num_layers, rows, KV, D] tensor")
-        self._check_keys(k_all[0])
+        """[Q2] All Quest layers in one launch; ``k_all`` is the pool's ``[model_layers, rows,
+        KV, D]`` tensor (``MHATokenToKVPool.k_all``) indexed by model layer id, so Quest layer
+        ``start_layer + i`` reads ``k_all[start_layer + i]``."""
+        self._check_k_all(k_all)
         stride = k_all.stride(0)
         self._prefill(k_all[self.start_layer], stride, k_all.shape[1], int(req_pool_idx),
                       prefill_indices, 0, self.num_layers, True)
+
+    def _check_k_all(self, k_all: torch.Tensor) -> None:
+        if k_all.dim() != 4 or not k_all.is_contiguous():
+            raise ValueError("k_all must be a contiguous [model_layers, rows, KV, D] tensor")
+        if k_all.shape[0] < self.end_layer:
+            raise ValueError(
+                f"k_all holds {k_all.shape[0]} layers but the Quest layers run to {self.end_layer}: "
+                "pass the pool's full per-model-layer tensor"
+            )
+        self._check_keys(k_all[0])
 
     def _prefill(self, k0, stride, rows, req, idx, layer_begin, n_layers, set_counters) -> None:
         idx = idx.to(self.device)
@@ -261,10 +270,9 @@ class QuestAlgorithm:
         self, req_indices: torch.Tensor, k_all: torch.Tensor, device_locs: torch.Tensor
     ) -> None:
         """[Q3] Fold for every layer and finalize completed pages in one pass
-        (update_decode_representations x layers + maybe_finalize_decode_representations)."""
-        if k_all.dim() != 4 or not k_all.is_contiguous():
-            raise ValueError("k_all must be a contiguous [num_layers, rows, KV, D] tensor")
-        self._check_keys(k_all[0])
+        (update_decode_representations x layers + maybe_finalize_decode_representations);
+        ``k_all`` as for update_prefill_representations_fused (indexed by model layer id)."""
+        self._check_k_all(k_all)
         self._decode(k_all[self.start_layer], k_all.stride(0), k_all.shape[1], req_indices,
                      device_locs, 0, self.num_layers, True)
 

@@ -37,3 +37,19 @@ def cuda():
     if not torch.cuda.is_available():
         pytest.skip("needs a GPU")
     return torch.device("cuda", 0)
+
+
+def attn_tol(ref: np.ndarray) -> float:
+    """Attention tolerance for bf16 outputs: the path's stated 2e-2 absolute bound, tightened
+    to the output's own scale.  The kernels' error sources (bf16 output rounding, bf16
+    softmax weights into the P.V product) stay below 0.5% of the largest output, while
+    dropping one 16-row step of 2048 rows moves outputs by about 2e-2."""
+    return min(2e-2, 1e-3 + 1e-2 * float(np.abs(ref).max()))
+
+
+def assert_attn_close(got, ref, msg: str = "") -> None:
+    got = np.asarray(got, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    err = float(np.abs(got - ref).max()) if ref.size else 0.0
+    tol = attn_tol(ref) if ref.size else 0.0
+    assert err <= tol, f"{msg}: max |err| {err:.3e} > {tol:.3e} (max |ref| {np.abs(ref).max():.3e})"

@@ -92,6 +92,40 @@ def test_swap_in_is_exact_under_random_selections(prefill_len, buf, top_k):
     assert stats.misses > 0 and (stats.hits, stats.misses) == (st.hits, st.misses)
 
 
+@pytest.mark.parametrize(("prefill_len", "buf", "top_k"), [(1200, 1025, 512), (2000, 1500, 1024), (5000, 4097, 2048)])
+def test_swap_in_large_buffers_match_oracle(prefill_len, buf, top_k):
+    """Hot buffers that are not a multiple of the plan block's 1024 threads and exceed it
+    (each thread holds a run of ceil(buf / 1024) LRU entries, the last runs partial or empty;
+    4097 is the benchmark's 4096 + 1): rows, buffer_tokens, lru_slots and hit/miss counts
+    equal the oracle's at every step, with duplicated and newest-token entries."""
+    steps = 24
+    total = prefill_len + steps
+    k, v = truth(total, seed=3)
+    _, coord, pool = make(buf, top_k, max_reqs=2, max_ctx=total + 8)
+    admit(coord, pool, 1, prefill_len, k, v)
+    st = oh.HiSparseState(LAYERS, 2, buf=buf, top_k=top_k, max_ctx=total + 8)
+    st.admit(1, np.arange(prefill_len))
+    gen = torch.Generator().manual_seed(17)
+    for pos in range(prefill_len, total):
+        reqs, seq_lens = decode_step(coord, 1, pos, k, v)
+        if pos > prefill_len:
+            st.backup(1, pos - 1, pos - 1)
+        seq_len = pos + 1
+        for layer in range(LAYERS):
+            # a recent run, a few far pages, random picks and a duplicate, like a Quest layout
+            sel = torch.randint(0, seq_len, (top_k,), generator=gen)
+            sel[: top_k // 4] = torch.arange(seq_len - top_k // 4, seq_len)
+            sel[top_k // 4] = sel[top_k // 4 + 1]
+            rows = coord.swap_in_selected_pages(reqs, seq_lens, sel[None].int(), layer)
+            ref_rows, _ = st.swap_in(layer, [1], [seq_len], sel[None].numpy())
+            assert np.array_equal(rows.cpu().numpy()[0], ref_rows[0]), f"layer {layer} pos {pos}"
+            assert np.array_equal(coord.buffer_tokens[layer, 1].cpu().numpy(), st.buffer_tokens[layer, 1])
+            assert np.array_equal(coord.lru_slots[layer, 1].cpu().numpy(), st.lru_slots[layer, 1])
+            assert torch.equal(coord.device_k[layer][rows[0]].cpu(), k[layer, sel])
+    stats = coord.stats
+    assert stats.misses > 0 and stats.hits > 0 and (stats.hits, stats.misses) == (st.hits, st.misses)
+
+
 def test_every_decoded_token_is_backed_up_to_host():
     k, v = truth(64)
     _, coord, pool = make(buf=8, top_k=8)
@@ -285,3 +319,185 @@ def test_quest_hisparse_is_bit_identical_to_quest(avoid, shape):
     assert fused == (shape == len(BIT_IDENTITY) - 1)
     assert torch.equal(poss["quest"], poss["quest_hisparse"])
     assert torch.equal(outs["quest"], outs["quest_hisparse"])
+
+
+def test_device_row_allocator_hands_out_rows_in_the_reference_order():
+    """The host tier's free list kept on the device gives the rows TokenToKVPoolAllocator
+    (reference memory.py:47-72) gives, over interleaved allocs and frees."""
+    from qwenquest_amd.hisparse.coordinator import DeviceRowAllocator
+    from qwenquest_amd.memory import TokenToKVPoolAllocator
+
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    dev = DeviceRowAllocator(50, DEV, err, 0)
+    ref = TokenToKVPoolAllocator(50, device="cpu")
+    gen = torch.Generator().manual_seed(3)
+    held = []
+    for step in range(40):
+        if held and torch.rand(1, generator=gen).item() < 0.4:
+            rows = held.pop(int(torch.randint(0, len(held), (1,), generator=gen)))
+            ref.free(rows)
+            dev.free(rows.to(DEV))
+        else:
+            n = int(torch.randint(1, 6, (1,), generator=gen))
+            if n > ref.available_size():
+                with pytest.raises(RuntimeError):
+                    dev.alloc(n)
+                continue
+            a, b = ref.alloc(n), dev.alloc(n).cpu()
+            assert torch.equal(a, b), f"step {step}"
+            held.append(a)
+        assert dev.available_size() == ref.available_size()
+
+
+def _his_coord(buf, top_k, ctx, host_pool, kv=2, d=8, dtype=torch.float32, max_reqs=2):
+    from qwenquest_amd.hisparse import HiSparseCoordinator
+    from qwenquest_amd.memory import MHATokenToKVPool
+    from qwenquest_amd.quest import QuestAlgorithm
+
+    quest = QuestAlgorithm(top_k=top_k, page_size=1, device=DEV)
+    quest.init_storage(0, 1, max_reqs, ctx, kv, d)
+    coord = HiSparseCoordinator(quest=quest, num_layers=1, kv_heads=kv, head_dim=d, max_reqs=max_reqs,
+                                max_context_len=ctx, top_k=top_k, device_buffer_size=buf,
+                                host_pool_size=host_pool, dtype=dtype, device=DEV)
+    pool = MHATokenToKVPool(max_reqs * ctx, 1, kv, d, dtype, DEV)
+    g = torch.Generator(device=DEV).manual_seed(8)
+    pool.k_all.normal_(generator=g)
+    pool.v_all.normal_(generator=g)
+    return coord, pool
+
+
+def test_host_pool_exhaustion_is_raised_from_the_device():
+    """The eager backup takes its host rows on the device: with the pool exhausted the step
+    backs nothing up and check_errors raises the allocator's RuntimeError (memory.py:62-66)."""
+    coord, pool = _his_coord(buf=8, top_k=4, ctx=64, host_pool=22)
+    coord.admit_request(0, 20, pool, torch.arange(1, 21, device=DEV))
+    reqs = torch.tensor([0], device=DEV)
+    for pos in (20, 21, 22):  # the first step is skipped, then two backups take the last 2 rows
+        coord.prepare_decode_step(reqs, torch.tensor([pos + 1], device=DEV))
+    coord.check_errors()
+    assert coord.host_allocator.available_size() == 0
+    coord.prepare_decode_step(reqs, torch.tensor([24], device=DEV))  # position 22: no row left
+    with pytest.raises(RuntimeError, match="out of memory"):
+        coord.check_errors()
+    assert int(coord.req_to_host_pool[0, 22]) == -1 and int(coord.req_to_host_pool[0, 21]) >= 0
+
+
+@pytest.mark.parametrize("fused", [True, False])
+def test_failed_swap_in_poisons_only_that_request(fused):
+    """A position without a host row (coordinator.py:284-286): the request's swap-in rows are
+    all -1 and its state is unchanged, the rows attention (the fused layer step's kernel and
+    the chunked one) outputs NaN for it and a finite output for the other request, and the
+    host sees the error through the pinned mirror without a device synchronisation."""
+    from qwenquest_amd.attention.ops import decode_attention_rows
+
+    H4, KV4, D4, buf, top_k, ctx, n = 32, 4, 128, 256, 128, 600, 400
+    coord, pool = _his_coord(buf, top_k, ctx, 2 * ctx, kv=KV4, d=D4, dtype=torch.bfloat16)
+    for r in (0, 1):
+        coord.admit_request(r, n, pool, torch.arange(1 + r * ctx, 1 + r * ctx + n, device=DEV))
+    reqs = torch.tensor([0, 1], device=DEV)
+    seq = torch.tensor([n + 1, n + 1], device=DEV)
+    coord.prepare_decode_step(reqs, seq)
+    newkv = torch.randn(2, KV4, D4, device=DEV).to(torch.bfloat16)
+    coord.write_new_token(0, reqs, seq, newkv, newkv)
+    coord.req_to_host_pool[1, 310] = -1
+    sel = torch.arange(n - top_k, n, device=DEV).repeat(2, 1).int()  # misses beyond the buffer, all backed up
+    tokens_before = coord.buffer_tokens[0, 1].clone()
+    rows = coord.swap_in_selected_pages(reqs, seq, sel, 0)
+    torch.cuda.synchronize()
+    assert bool((rows[1] == -1).all()) and bool((rows[0] >= 0).all())
+    assert torch.equal(coord.buffer_tokens[0, 1], tokens_before)
+    with pytest.raises(AssertionError):
+        coord.check_errors(sync=False)
+    coord.check_errors()  # raised once: both the word and its mirror are cleared
+    q = torch.randn(2, H4, D4, device=DEV).to(torch.bfloat16)
+    actual = torch.full((2,), top_k, dtype=torch.int32, device=DEV)
+    sync = torch.zeros(int(_lib.load().qq_quest_layer_step_sync_bytes(2, KV4)), dtype=torch.uint8, device=DEV)
+    out = decode_attention_rows(q, coord.device_k[0], coord.device_v[0], rows, actual, D4**-0.5,
+                                sync=sync if fused else None).float()
+    assert bool(torch.isnan(out[1]).all()), "the failed request's output is not NaN"
+    assert bool(torch.isfinite(out[0]).all())
+
+
+def test_quest_hisparse_step_in_a_graph_equals_eager():
+    """The quest_hisparse decode step has no host synchronisation: captured once in a HIP graph
+    (bounds fold + eager backup + per layer new token, selection, swap-in, attention) and
+    replayed, it gives the eager run's outputs, positions, LRU state, host rows and counters
+    bit for bit over 12 steps, while the hot buffer swaps."""
+    from qwenquest_amd.attention.quest_hisparse import QuestHiSparseBackend
+    from qwenquest_amd.batch import ForwardBatch, ForwardMode
+    from qwenquest_amd.memory import MHATokenToKVPool, ReqToTokenPool
+
+    H4, KV4, D4, TOPK, PAGE, BUF, CTX, L4, steps = 32, 4, 128, 256, 64, 384, 1200, 2, 12
+    prompts = {0: 700, 1: 1003}
+    kk = torch.randn(L4, 2 * CTX + 1, KV4, D4, generator=torch.Generator().manual_seed(61)).to(torch.bfloat16)
+    vv = torch.randn(L4, 2 * CTX + 1, KV4, D4, generator=torch.Generator().manual_seed(62)).to(torch.bfloat16)
+
+    def setup():
+        rtp = ReqToTokenPool(2, CTX, DEV)
+        kvp = MHATokenToKVPool(2 * CTX, L4, KV4, D4, torch.bfloat16, DEV)
+        kvp.k_all.copy_(kk.to(DEV))
+        kvp.v_all.copy_(vv.to(DEV))
+        for r in (0, 1):
+            rtp.req_to_token[r] = torch.arange(1 + r * CTX, 1 + (r + 1) * CTX, dtype=torch.int32)
+        be = QuestHiSparseBackend(rtp, kvp, {"algorithm": "quest", "top_k": TOPK, "quest_page_size": PAGE,
+                                             "device_buffer_size": BUF}, host_pool_size=2 * CTX)
+        pre = ForwardBatch(ForwardMode.EXTEND, None, None, torch.tensor([0, 1]),
+                           torch.tensor([prompts[0], prompts[1]]), None, rtp, kvp, be)
+        be.on_extend_finished(pre)
+        return rtp, kvp, be
+
+    class Lay:
+        def __init__(self, i):
+            self.layer_id, self.scaling = i, D4**-0.5
+
+    qs = torch.randn(steps, L4, 2, H4, D4, generator=torch.Generator().manual_seed(63)).to(torch.bfloat16).to(DEV)
+    ks = torch.randn(steps, L4, 2, KV4, D4, generator=torch.Generator().manual_seed(64)).to(torch.bfloat16).to(DEV)
+    results = {}
+    for mode in ("eager", "graph"):
+        rtp, kvp, be = setup()
+        seq = torch.tensor([prompts[0] + 1, prompts[1] + 1], device=DEV, dtype=torch.int64)
+        q_in = torch.empty_like(qs[0])
+        k_in = torch.empty_like(ks[0])
+        batch = ForwardBatch(ForwardMode.DECODE, None, None, torch.tensor([0, 1], device=DEV), seq, None, rtp, kvp, be)
+        outs_static, pos_static = [], []
+
+        def step():
+            be.init_forward_metadata(batch)
+            res = []
+            for layer in range(L4):
+                res.append(be.forward_decode(q_in[layer], k_in[layer], k_in[layer], Lay(layer), batch))
+            return res
+
+        outs, poss = [], []
+        graph = None
+        for t in range(steps):
+            q_in.copy_(qs[t])
+            k_in.copy_(ks[t])
+            if mode == "eager" or t < 2:  # two eager steps first (workspaces, first-step skips)
+                res = step()
+            else:
+                if graph is None:
+                    torch.cuda.synchronize()
+                    graph = torch.cuda.CUDAGraph()
+                    with torch.cuda.graph(graph):
+                        outs_static = step()
+                graph.replay()
+                res = outs_static
+            torch.cuda.synchronize()
+            outs.append(torch.stack([o.clone() for o in res]).cpu())
+            poss.append(be._positions[:2].clone().cpu())
+            seq.add_(1)
+        coord = be.coord
+        results[mode] = (torch.stack(outs), torch.stack(poss), coord.buffer_tokens.cpu(), coord.lru_slots.cpu(),
+                         coord.req_to_host_pool.cpu(), coord.host_k_all.clone(), coord._stats.cpu(),
+                         coord.host_allocator.available_size())
+        del rtp, kvp, be, coord
+        torch.cuda.empty_cache()
+    e, g = results["eager"], results["graph"]
+    for t in range(steps):
+        assert torch.equal(e[1][t], g[1][t]), f"step {t}: positions"
+        assert torch.equal(e[0][t].view(torch.int16), g[0][t].view(torch.int16)), f"step {t}: outputs"
+    for i, what in enumerate(("buffer_tokens", "lru_slots", "req_to_host_pool", "host tier", "counters"), start=2):
+        assert torch.equal(e[i], g[i]), what
+    assert e[7] == g[7]
+    assert int(e[6][1]) > 0  # the hot buffer swapped

@@ -1,8 +1,9 @@
 """GPU parity of the Quest path (bounds, GQA mean, scores, selection, attention)
 against the CPU oracle on identical seeded inputs.
 
-Bounds, scores (canonical order), positions: bit-exact.  Attention: 2e-2 abs
-in bf16, 1e-4 abs in fp32 (the tolerances stated for the path).
+Bounds, scores (canonical order), positions: bit-exact.  Attention: 1e-4 abs in fp32;
+in bf16 the stated 2e-2 abs, tightened to 1e-3 + 1% of the largest output
+(tests.conftest.attn_tol).
 """
 
 from __future__ import annotations
@@ -14,7 +15,7 @@ import torch
 from oracle import attention as oa
 from oracle import bf16
 from oracle import quest as oq
-from tests.conftest import bf16_bits, load_golden
+from tests.conftest import assert_attn_close, bf16_bits, load_golden
 
 pytestmark = pytest.mark.gpu
 
@@ -85,6 +86,39 @@ def test_prefill_fused_over_layers_equals_per_layer():
     assert torch.equal(a.page_k_bounds, b.page_k_bounds)
     assert torch.equal(a.running_k_min, b.running_k_min)
     assert torch.equal(a.running_token_count, b.running_token_count)
+
+
+def test_fused_bounds_with_start_layer_read_the_model_layers():
+    """A backend covering model layers 2..3 of a 4-layer pool: the fused prefill and decode
+    fold read k_all[2] and k_all[3] (the pool is indexed by model layer id), equal to the
+    per-layer calls; a k_all holding fewer layers than end_layer is refused."""
+    from qwenquest_amd.memory import MHATokenToKVPool
+    from qwenquest_amd.quest import QuestAlgorithm
+
+    kvp = MHATokenToKVPool(600, 4, 2, 16, torch.bfloat16, DEV)
+    kvp.k_all.copy_(rand_bf16((4, 601, 2, 16), seed=13).to(DEV))
+    a = QuestAlgorithm(top_k=64, page_size=16, device=DEV)
+    b = QuestAlgorithm(top_k=64, page_size=16, device=DEV)
+    for qa in (a, b):
+        qa.init_storage(2, 4, 2, 600, 2, 16)
+    idx = torch.arange(1, 300, device=DEV)
+    a.update_prefill_representations_fused(1, kvp.k_all, idx)
+    for layer in (2, 3):
+        b.update_prefill_representations(layer, 1, kvp.k_buffer[layer], idx)
+    reqs = torch.tensor([1], device=DEV)
+    for step in range(20):
+        locs = torch.tensor([300 + step], device=DEV)
+        a.update_decode_representations_fused(reqs, kvp.k_all, locs)
+        for layer in (2, 3):
+            b.update_decode_representations(layer, reqs, kvp.k_buffer[layer], locs)
+        b.maybe_finalize_decode_representations(reqs)
+    torch.cuda.synchronize()
+    assert torch.equal(a.page_k_bounds, b.page_k_bounds)
+    assert torch.equal(a.running_k_min, b.running_k_min) and torch.equal(a.running_k_max, b.running_k_max)
+    assert torch.equal(a.running_token_count, b.running_token_count)
+    assert torch.equal(a.running_page_idx, b.running_page_idx)
+    with pytest.raises(ValueError, match="layers"):
+        a.update_prefill_representations_fused(0, kvp.k_all[:3].contiguous(), idx)
 
 
 @pytest.mark.parametrize("fused", [False, True])
@@ -337,6 +371,8 @@ def attention_case(dtype, heads, kv, d, n_rows, seed, dup=False):
 @pytest.mark.parametrize("heads,kv,d", [(32, 4, 128), (8, 2, 16), (16, 4, 32), (4, 4, 8)])
 def test_attention_matches_oracle(dtype, tol, heads, kv, d):
     out, ref = attention_case(dtype, heads, kv, d, [2048, 1, 65, 700], seed=heads + d, dup=True)
+    if dtype == torch.bfloat16:
+        assert_attn_close(out, ref, f"{heads}/{kv} heads x {d}")
     assert np.abs(out - ref).max() < tol
 
 
@@ -411,7 +447,7 @@ def test_quest_backend_decode_steps_match_oracle():
                 assert np.array_equal(pos[i, :n], ref_pos[i, :n]), f"step {step} layer {layer} req {r}"
             rows = [1 + r * CTX + ref_pos[i, : int(ref_actual[i])] for i, r in enumerate(reqs)]
             ref = oa.sparse_decode(q.float().numpy(), kb[layer], vb[layer], rows, D**-0.5)
-            assert np.abs(out.float().cpu().numpy() - ref).max() < 2e-2
+            assert_attn_close(out.float().cpu().numpy(), ref, f"step {step} layer {layer}")
     assert_state_equal(be.quest, st)
 
 
@@ -514,7 +550,7 @@ def test_forward_decode_fused_path_engine_flow(flow):
                     assert np.array_equal(rec[i].positions.numpy(), ref_pos[i, :n]), f"step {step} L{layer} r{r}"
                 rows = [1 + r * CTX + ref_pos[i, : int(ref_actual[i])] for i, r in enumerate(reqs)]
                 ref = oa.sparse_decode(q.float().numpy(), kb[layer], vb[layer], rows, D**-0.5)
-                assert np.abs(out.float().cpu().numpy() - ref).max() < 2e-2
+                assert_attn_close(out.float().cpu().numpy(), ref, f"step {step} layer {layer}")
         assert_state_equal(be.quest, st)
         # the new tokens really went to the pool
         torch.cuda.synchronize()
@@ -531,7 +567,7 @@ R2T_LAYOUTS = ("page_runs", "scattered", "mixed")
 def test_fused_step_req_to_token_layouts(layout, ctx):
     """The fused layer step over req_to_token layouts that are not one run per request:
     pages as runs at shuffled bases, scattered rows, and page runs broken by swapped rows.
-    Positions bit-exact vs the oracle, outputs within 2e-2 of the oracle's attention over
+    Positions bit-exact vs the oracle, outputs within attn_tol of the oracle's attention over
     r2t[req, positions].  The long tables (2304 and 3072 pages) take the selection's 9- and
     12-keys-per-thread forms."""
     from qwenquest_amd.attention.quest_only import QuestOnlyBackend
@@ -598,7 +634,7 @@ def test_fused_step_req_to_token_layouts(layout, ctx):
             assert np.array_equal(got_pos[i, :n], ref_pos[i, :n]), f"step {step} r{r}"
             rows.append(r2t[r, ref_pos[i, :n]].astype(np.int64))
         ref = oa.sparse_decode(q.float().numpy(), kb[0], vb[0], rows, D**-0.5)
-        assert np.abs(out.float().cpu().numpy() - ref).max() < 2e-2
+        assert_attn_close(out.float().cpu().numpy(), ref, f"step {step}")
     assert not step_counters(be, len(reqs)).any()
 
 
@@ -640,14 +676,14 @@ def test_positions_and_rows_entries_are_bit_identical():
     for i in (0, 2, 3):
         r = rows[i, : int(actual[i])].numpy()
         ref = oa.decode_attention(q[i].float().numpy(), kb[r], vb[r], D**-0.5)
-        assert np.abs(got[i] - ref).max() < 2e-2
+        assert_attn_close(got[i], ref, f"request {i}")
     assert not got[1].any()  # no rows: zeros
 
 
 def test_fused_layer_step_graph_replay_eager_and_four_launch_agree():
     """The fused (two-launch) layer step replayed from a HIP graph equals its eager run bit for bit
     (positions and outputs, every replay), the four-launch path gives the same positions
-    and outputs within 2e-2, and the sync counters are back at zero after each step."""
+    and outputs within attn_tol, and the sync counters are back at zero after each step."""
     from qwenquest_amd.attention.quest_only import QuestOnlyBackend
     from qwenquest_amd.batch import ForwardBatch, ForwardMode
     from qwenquest_amd.memory import MHATokenToKVPool, ReqToTokenPool
@@ -717,4 +753,4 @@ def test_fused_layer_step_graph_replay_eager_and_four_launch_agree():
     for i, ((oe, pe), (og, pg), (of, pf)) in enumerate(zip(runs["eager"], runs["graph"], runs["four"])):
         assert torch.equal(pe, pg) and torch.equal(oe, og), f"graph replay {i} differs from eager"
         assert torch.equal(pe, pf), f"step {i}: four-launch positions differ"
-        assert (oe.float() - of.float()).abs().max().item() < 2e-2, f"step {i}"
+        assert_attn_close(of.float().cpu().numpy(), oe.float().cpu().numpy(), f"step {i}: four-launch vs fused")
