@@ -13,7 +13,11 @@ req_to_token gather and attention.  The step is captured once in a HIP graph
 and replayed; seq_lens advance by one token per replay, so pages complete and
 get finalized during the run.  Reported value: microseconds per layer-step
 (step time / 48).  The roofline's `traffic` is read from the committed
-rocprofv3 PMC summary in profiles/ (copy-calibrated FETCH_SIZE + WRITE_SIZE).
+rocprofv3 PMC summary in profiles/ (copy-calibrated FETCH_SIZE + WRITE_SIZE),
+and only when the summary records the hash of the HIP sources this build has.
+After the timed region the same line gets `cpu_baseline` (the reference's op
+sequence in torch on the host cores, on the GPU's own layer-0 tensors) and
+`hisparse` (the quest_hisparse tier below, 4 layers, graph-replayed).
 
     python bench.py [--steps K] [--warmup W]
 
@@ -165,19 +169,22 @@ def pinned_h2d_peak(nbytes: int = 1 << 30, reps: int = 5) -> float:
     return nbytes * reps / (e0.elapsed_time(e1) * 1e-3) / 1e9
 
 
-def hisparse_bench(args) -> int:
-    """quest_hisparse decode (QuestHiSparseBackend, the drop-in path), swap-in measured with
-    HIP events around each swap-in call on the launch stream."""
+def hisparse_measure(B: int, S: int, L: int, warmup: int, steps: int, event_steps: int) -> dict:
+    """quest_hisparse decode (QuestHiSparseBackend, the drop-in path) at batch B x S tokens, a
+    hot buffer of 4096 + 1 rows per request and layer, the K/V history of L layers in pinned
+    host memory, queries AR(1) with rho 0.9 across steps.  After `warmup` eager steps, one
+    decode step (bounds fold + eager backup + per layer new token, selection, swap-in and
+    attention) is captured in a HIP graph and replayed for `steps` timed steps (µs per
+    layer-step); `event_steps` more steps run eagerly with HIP events around every swap-in
+    call (plan + copy) on the launch stream, for the swap-in time and the missed rows."""
     from qwenquest_amd.attention.quest_hisparse import QuestHiSparseBackend
     from qwenquest_amd.batch import ForwardBatch, ForwardMode
     from qwenquest_amd.memory import MHATokenToKVPool, ReqToTokenPool
 
     dev = torch.device("cuda", 0)
-    torch.cuda.set_device(dev)
-    B, S, L = args.batch, args.ctx, args.hisparse_layers
     H, KV, D, P, TOP_K, BUF = 32, 4, 128, 64, 2048, 4096
-    steps = args.warmup + args.steps
-    max_ctx = S + steps + 64
+    total = warmup + steps + event_steps + 2
+    max_ctx = S + total + 64
     t_setup = time.perf_counter()
     rtp = ReqToTokenPool(B, max_ctx, dev)
     kvp = MHATokenToKVPool(B * max_ctx, L, KV, D, torch.bfloat16, dev)
@@ -196,66 +203,107 @@ def hisparse_bench(args) -> int:
     setup_s = time.perf_counter() - t_setup
 
     coord = be.coord
+    layers = [Layer(i, D**-0.5) for i in range(L)]
+    rho = 0.9
+    q = torch.randn((L, B, H, D), generator=gen, device=dev)
+    q_in = torch.empty((L, B, H, D), dtype=torch.bfloat16, device=dev)
+    kv_in = torch.empty((2, L, B, KV, D), dtype=torch.bfloat16, device=dev)
+    seq = torch.full((B,), S, device=dev, dtype=torch.int64)
+    batch = ForwardBatch(ForwardMode.DECODE, None, None, torch.arange(B, device=dev), seq, None, rtp, kvp, be)
+
+    def next_inputs():
+        q.mul_(rho).add_(torch.randn((L, B, H, D), generator=gen, device=dev), alpha=(1 - rho**2) ** 0.5)
+        q_in.copy_(q)
+        kv_in.copy_(torch.randn((2, L, B, KV, D), generator=gen, device=dev))
+
+    def step():
+        be.init_forward_metadata(batch)
+        return [be.forward_decode(q_in[i], kv_in[0, i], kv_in[1, i], layers[i], batch) for i in range(L)]
+
+    for _ in range(warmup):
+        next_inputs()
+        step()
+        seq.add_(1)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    step_ms = []
+    m0 = coord.stats.misses
+    for _ in range(steps):
+        next_inputs()
+        e0.record(stream)
+        graph.replay()
+        e1.record(stream)
+        e1.synchronize()
+        step_ms.append(e0.elapsed_time(e1))
+        seq.add_(1)
+    graph_misses = coord.stats.misses - m0
+    # eager steps with events around the swap-in calls
     swap = coord.swap_in_selected_pages
     events = []
 
     def timed_swap(*a, **kw):
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
+        s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s0.record()
         rows = swap(*a, **kw)
-        e1.record()
-        events.append((e0, e1))
+        s1.record()
+        events.append((s0, s1))
         return rows
 
     coord.swap_in_selected_pages = timed_swap
-    layers = [Layer(i, D**-0.5) for i in range(L)]
-    rho = 0.9
-    q = torch.randn((L, B, H, D), generator=gen, device=dev)
-    seq = torch.full((B,), S, device=dev, dtype=torch.int64)
-    rpi = torch.arange(B, device=dev, dtype=torch.int64)
-    step_ms, swap_ms, misses = [], [], []
-    for step in range(steps):
-        q = rho * q + (1 - rho**2) ** 0.5 * torch.randn((L, B, H, D), generator=gen, device=dev)
-        qb = q.to(torch.bfloat16)
-        kn = torch.randn((L, B, KV, D), generator=gen, device=dev).to(torch.bfloat16)
-        vn = torch.randn((L, B, KV, D), generator=gen, device=dev).to(torch.bfloat16)
+    swap_ms, misses = [], []
+    for _ in range(event_steps):
+        next_inputs()
         m0 = coord.stats.misses
         events.clear()
-        batch = ForwardBatch(ForwardMode.DECODE, None, None, rpi, seq, None, rtp, kvp, be)
+        step()
         torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        be.init_forward_metadata(batch)
-        for layer in range(L):
-            be.forward_decode(qb[layer], kn[layer], vn[layer], layers[layer], batch)
-        e1.record()
-        e1.synchronize()
-        if step >= args.warmup:
-            step_ms.append(e0.elapsed_time(e1))
-            swap_ms.append(sum(a.elapsed_time(b) for a, b in events))
-            misses.append(coord.stats.misses - m0)
+        swap_ms.append(sum(a.elapsed_time(b) for a, b in events))
+        misses.append(coord.stats.misses - m0)
         seq.add_(1)
+    coord.swap_in_selected_pages = swap
     row_bytes = 2 * KV * D * 2  # K + V row
     miss_rows = float(np.mean(misses)) / L
     swap_us = float(np.mean(swap_ms)) * 1e3 / L
     h2d = miss_rows * row_bytes / (swap_us * 1e-6) / 1e9 if swap_us > 0 else 0.0
     peak = pinned_h2d_peak()
     st = coord.stats
-    print(json.dumps({
-        "metric": "quest_hisparse decode @128K ctx, batch 16: swap-in H2D GB/s and us per layer-step",
-        "value": round(h2d, 2), "unit": "GB/s (swap-in misses x 2 KiB / swap-in time)",
-        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
-        "dtype": "bf16", "data": "synthetic N(0,1) K/V, AR(1) queries rho 0.9, fixed seeds",
-        "config": {"workload": f"quest_hisparse decode, batch {B}, {S}-token context, hot buffer {BUF}+1 rows, "
-                               f"{L} layers resident in pinned host memory", "batch": B, "seq_len": S, "layers": L},
+    res = {
         "us_per_layer_step": round(float(np.mean(step_ms)) * 1e3 / L, 2),
-        "swap_in_us_per_layer_step": round(swap_us, 2),
+        "graph": True,
         "swap_in_rows_per_layer_step": round(miss_rows, 1),
-        "hit_rate": round(st.hit_rate, 4),
+        "graph_swap_in_rows_per_layer_step": round(graph_misses / steps / L, 1),
+        "swap_in_us_per_layer_step": round(swap_us, 2),
+        "h2d_gbs": round(h2d, 2),
         "h2d_pinned_memcpy_peak_gbs": round(peak, 2),
         "h2d_frac_of_memcpy_peak": round(h2d / peak, 4) if peak > 0 else None,
         "h2d_frac_of_64gbs_nominal": round(h2d / 64.0, 4),
+        "hit_rate": round(st.hit_rate, 4),
+        "workload": f"quest_hisparse decode, batch {B}, {S}-token context, hot buffer {BUF}+1 rows, {L} layers' "
+                    f"history in pinned host memory (the per-layer work is the same for all 48), AR(1) queries "
+                    f"rho 0.9; {warmup} warm-up steps, {steps} graph-replayed timed steps, {event_steps} eager "
+                    f"steps with events around the swap-in",
         "setup_s": round(setup_s, 1),
+    }
+    del be, coord, kvp, rtp, graph
+    torch.cuda.empty_cache()
+    return res
+
+
+def hisparse_bench(args) -> int:
+    torch.cuda.set_device(0)
+    r = hisparse_measure(args.batch, args.ctx, args.hisparse_layers, args.warmup, args.steps, args.steps)
+    print(json.dumps({
+        "metric": "quest_hisparse decode @128K ctx, batch 16: swap-in H2D GB/s and us per layer-step",
+        "value": r["h2d_gbs"], "unit": "GB/s (swap-in misses x 2 KiB / swap-in time)",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
+        "dtype": "bf16", "data": "synthetic N(0,1) K/V, AR(1) queries rho 0.9, fixed seeds",
+        "config": {"workload": r["workload"], "batch": args.batch, "seq_len": args.ctx,
+                   "layers": args.hisparse_layers},
+        **{k: v for k, v in r.items() if k != "workload"},
     }))
     return 0
 
@@ -354,6 +402,8 @@ def main() -> int:
                     help="contexts drawn uniform in [8192, ctx] per request (seeded) instead of all ctx")
     ap.add_argument("--hisparse", action="store_true", help="measure the quest_hisparse tier instead")
     ap.add_argument("--hisparse-layers", type=int, default=4)
+    ap.add_argument("--hisparse-steps", type=int, default=48,
+                    help="graph-replayed quest_hisparse steps measured after the headline (0 = skip)")
     ap.add_argument("--dense", action="store_true",
                     help="measure dense decode (every request attends its whole context) instead")
     ap.add_argument("--dense-layers", type=int, default=8, help="K/V pools of the dense run (cycled)")
@@ -525,6 +575,14 @@ def main() -> int:
         "cpu_baseline": cpu,
         "setup_s": round(setup_s, 1),
     }
+    if args.hisparse_steps > 0 and not args.ragged:
+        # the quest_hisparse tier, measured after and outside the headline's timed region
+        del be, kvp, rtp, batch, q_all, k_new, v_new
+        if not args.no_graph:
+            del graph, run
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        line["hisparse"] = hisparse_measure(B, S, args.hisparse_layers, 32, args.hisparse_steps, 32)
     print(json.dumps(line))
     return 0
 
