@@ -51,6 +51,7 @@ constexpr int kMaxParts = 8;         // dense decode: parts merged in one pass
 constexpr int kW4Waves = 4;
 constexpr int kW4Parts = 8;
 constexpr int kW4RowCap = 1024;
+constexpr int kUnitWaves = 4;
 
 struct StepArgs {
   SelectArgs s;            // scoring, selection, positions, new token
@@ -175,6 +176,147 @@ struct HeadSmem {
   float l[W][kStepMaxG];
   float o[W][kStepMaxG][kMfmaDim];
 };
+
+// The end of an attention block: its W waves' (M, L, o) (o[e][i]: head 4hi + i,
+// channel 8lo + e) combined in LDS; with one part the block writes the output,
+// else an (m, l, o) partial (agent scope) and the block that completes the
+// (request, KV head) count merges the parts (up to MG at once; GROUPED: more in
+// groups of MG, maximum first).  poison: the output becomes NaN.
+template <int W, int MG, bool GROUPED>
+__device__ inline void finish_block(const StepArgs& a, int bh, int part, float M, float L, const float4_t (&o)[8],
+                                    bool poison, float (*sm_m)[kStepMaxG], float (*sm_l)[kStepMaxG],
+                                    float (*sm_o)[kStepMaxG][kMfmaDim], uint32_t* s_last) {
+  const SelectArgs& sa = a.s;
+  constexpr int kThreads = 64 * W;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int lo = lane & 15, hi = lane >> 4;
+  const int parts = a.parts;
+  const int b = bh / kStepKV, h = bh - b * kStepKV;
+  const int G = a.G;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int head = hi * 4 + i;
+    if (head < G) {
+      float* dst = &sm_o[wave][head][lo * 8];
+      *reinterpret_cast<float4*>(dst) = make_float4(o[0][i], o[1][i], o[2][i], o[3][i]);
+      *reinterpret_cast<float4*>(dst + 4) = make_float4(o[4][i], o[5][i], o[6][i], o[7][i]);
+    }
+  }
+  if (hi == 0 && lo < G) {
+    sm_m[wave][lo] = M;
+    sm_l[wave][lo] = poison ? __builtin_nanf("") : L;  // NaN survives every weight of the merge
+  }
+  __syncthreads();
+  uint16_t* outp = a.out + (int64_t)b * sa.H * kMfmaDim + (int64_t)h * G * kMfmaDim;
+  const int64_t part_idx = (int64_t)bh * parts + part;
+  for (int idx = tid; idx < G * kMfmaDim; idx += kThreads) {
+    const int head = idx >> 7, d = idx & 127;
+    float Mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < W; ++w) Mx = fmaxf(Mx, sm_m[w][head]);
+    float Ls = 0.0f, Os = 0.0f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      const float mw = sm_m[w][head];
+      const float wgt = mw == -INFINITY ? 0.0f : exp2f(mw - Mx);
+      Ls += wgt * sm_l[w][head];
+      Os += wgt * sm_o[w][head][d];
+    }
+    if (parts == 1) {
+      outp[idx] = f2bf(!(Ls <= 0.0f) ? Os / Ls : 0.0f);  // NaN (a poisoned part) stays NaN
+    } else {
+      st_agent(a.part_o + (part_idx * G + head) * kMfmaDim + d, Os);
+      if (d == 0) {
+        st_agent(a.part_ml + (part_idx * G + head) * 2, Mx);
+        st_agent(a.part_ml + (part_idx * G + head) * 2 + 1, Ls);
+      }
+    }
+  }
+  if (parts == 1) return;
+  wait_memory();
+  __syncthreads();
+  if (tid == 0) *s_last = add_agent(attn_count(a, bh), 1u) == (uint32_t)(parts - 1);
+  __syncthreads();
+  if (!*s_last) return;
+  if (tid == 0) st_agent(attn_count(a, bh), 0u);
+  // merge the parts (in part order: the maximum of the parts' m first, then the
+  // weighted sums): each thread one head x 4 channels; up to MG parts all loads
+  // in flight at once, more parts (dense decode) in two passes of groups
+  const int64_t part0 = (int64_t)bh * parts;
+  const __amdgpu_buffer_rsrc_t ro =
+      agent_rsrc(a.part_o + part0 * G * kMfmaDim, (uint32_t)(parts * G * kMfmaDim * sizeof(float)));
+  const uint64_t* ml64 = reinterpret_cast<const uint64_t*>(a.part_ml) + part0 * G;
+  for (int grp = tid; grp < G * (kMfmaDim / 4); grp += kThreads) {
+    const int head = grp >> 5, d4 = (grp & 31) * 4;
+    float Mx = -INFINITY;
+    float Ls = 0.0f;
+    float4 Os = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (!GROUPED || parts <= MG) {
+      float4 ov[MG];
+      uint64_t mlv[MG];
+#pragma unroll
+      for (int j = 0; j < MG; ++j) {
+        if (j < parts) {
+          ov[j] = ld_agent_x4(ro, (uint32_t)(((j * G + head) * kMfmaDim + d4) * sizeof(float)));
+          mlv[j] = ld_agent(ml64 + j * G + head);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < MG; ++j)
+        if (j < parts) Mx = fmaxf(Mx, __uint_as_float((uint32_t)mlv[j]));
+#pragma unroll
+      for (int j = 0; j < MG; ++j) {
+        if (j < parts) {
+          const float mj = __uint_as_float((uint32_t)mlv[j]);
+          const float wgt = mj == -INFINITY ? 0.0f : exp2f(mj - Mx);
+          Ls += wgt * __uint_as_float((uint32_t)(mlv[j] >> 32));
+          Os.x += wgt * ov[j].x;
+          Os.y += wgt * ov[j].y;
+          Os.z += wgt * ov[j].z;
+          Os.w += wgt * ov[j].w;
+        }
+      }
+    } else {
+      for (int j0 = 0; j0 < parts; j0 += MG) {
+        uint64_t mlv[MG];
+#pragma unroll
+        for (int j = 0; j < MG; ++j)
+          if (j0 + j < parts) mlv[j] = ld_agent(ml64 + (j0 + j) * G + head);
+#pragma unroll
+        for (int j = 0; j < MG; ++j)
+          if (j0 + j < parts) Mx = fmaxf(Mx, __uint_as_float((uint32_t)mlv[j]));
+      }
+      for (int j0 = 0; j0 < parts; j0 += MG) {
+        float4 ov[MG];
+        uint64_t mlv[MG];
+#pragma unroll
+        for (int j = 0; j < MG; ++j) {
+          if (j0 + j < parts) {
+            ov[j] = ld_agent_x4(ro, (uint32_t)((((j0 + j) * G + head) * kMfmaDim + d4) * sizeof(float)));
+            mlv[j] = ld_agent(ml64 + (j0 + j) * G + head);
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < MG; ++j) {
+          if (j0 + j < parts) {
+            const float mj = __uint_as_float((uint32_t)mlv[j]);
+            const float wgt = mj == -INFINITY ? 0.0f : exp2f(mj - Mx);
+            Ls += wgt * __uint_as_float((uint32_t)(mlv[j] >> 32));
+            Os.x += wgt * ov[j].x;
+            Os.y += wgt * ov[j].y;
+            Os.z += wgt * ov[j].z;
+            Os.w += wgt * ov[j].w;
+          }
+        }
+      }
+    }
+    const bool any = !(Ls <= 0.0f);  // NaN (a poisoned part) stays NaN
+    const uint32_t lo2 = (uint32_t)f2bf(any ? Os.x / Ls : 0.0f) | ((uint32_t)f2bf(any ? Os.y / Ls : 0.0f) << 16);
+    const uint32_t hi2 = (uint32_t)f2bf(any ? Os.z / Ls : 0.0f) | ((uint32_t)f2bf(any ? Os.w / Ls : 0.0f) << 16);
+    *reinterpret_cast<uint2*>(outp + head * kMfmaDim + d4) = make_uint2(lo2, hi2);
+  }
+}
 
 // Attention of one (request, KV head, part) by a block of W waves: the block's
 // share of the layout slots, per_wave rows per wave in steps of 16T rows
@@ -309,129 +451,7 @@ __device__ inline void attend_item(const StepArgs& a, int bh, int part, unsigned
       attend_step<T>(ring[j], qb, r_end - (r0 + kStep * i), a.sl2, M, L, o, lo, hi);
     }
   }
-  // combine the waves in LDS
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int head = hi * 4 + i;
-    if (head < G) {
-      float* dst = &sm.o[wave][head][lo * 8];
-      *reinterpret_cast<float4*>(dst) = make_float4(o[0][i], o[1][i], o[2][i], o[3][i]);
-      *reinterpret_cast<float4*>(dst + 4) = make_float4(o[4][i], o[5][i], o[6][i], o[7][i]);
-    }
-  }
-  if (hi == 0 && lo < G) {
-    sm.m[wave][lo] = M;
-    sm.l[wave][lo] = poison ? __builtin_nanf("") : L;  // NaN survives every weight of the merge
-  }
-  __syncthreads();
-  uint16_t* outp = a.out + (int64_t)b * sa.H * kMfmaDim + (int64_t)h * G * kMfmaDim;
-  const int64_t part_idx = (int64_t)bh * parts + part;
-  for (int idx = tid; idx < G * kMfmaDim; idx += kThreads) {
-    const int head = idx >> 7, d = idx & 127;
-    float Mx = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < W; ++w) Mx = fmaxf(Mx, sm.m[w][head]);
-    float Ls = 0.0f, Os = 0.0f;
-#pragma unroll
-    for (int w = 0; w < W; ++w) {
-      const float mw = sm.m[w][head];
-      const float wgt = mw == -INFINITY ? 0.0f : exp2f(mw - Mx);
-      Ls += wgt * sm.l[w][head];
-      Os += wgt * sm.o[w][head][d];
-    }
-    if (parts == 1) {
-      outp[idx] = f2bf(!(Ls <= 0.0f) ? Os / Ls : 0.0f);  // NaN (a poisoned part) stays NaN
-    } else {
-      st_agent(a.part_o + (part_idx * G + head) * kMfmaDim + d, Os);
-      if (d == 0) {
-        st_agent(a.part_ml + (part_idx * G + head) * 2, Mx);
-        st_agent(a.part_ml + (part_idx * G + head) * 2 + 1, Ls);
-      }
-    }
-  }
-  if (parts == 1) return;
-  wait_memory();
-  __syncthreads();
-  if (tid == 0) *s_last = add_agent(attn_count(a, bh), 1u) == (uint32_t)(parts - 1);
-  __syncthreads();
-  if (!*s_last) return;
-  if (tid == 0) st_agent(attn_count(a, bh), 0u);
-  // merge the parts (in part order: the maximum of the parts' m first, then the
-  // weighted sums): each thread one head x 4 channels; up to MG parts all loads
-  // in flight at once, more parts (dense decode) in two passes of groups
-  const int64_t part0 = (int64_t)bh * parts;
-  const __amdgpu_buffer_rsrc_t ro =
-      agent_rsrc(a.part_o + part0 * G * kMfmaDim, (uint32_t)(parts * G * kMfmaDim * sizeof(float)));
-  const uint64_t* ml64 = reinterpret_cast<const uint64_t*>(a.part_ml) + part0 * G;
-  for (int grp = tid; grp < G * (kMfmaDim / 4); grp += kThreads) {
-    const int head = grp >> 5, d4 = (grp & 31) * 4;
-    float Mx = -INFINITY;
-    float Ls = 0.0f;
-    float4 Os = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (!GROUPED || parts <= MG) {
-      float4 ov[MG];
-      uint64_t mlv[MG];
-#pragma unroll
-      for (int j = 0; j < MG; ++j) {
-        if (j < parts) {
-          ov[j] = ld_agent_x4(ro, (uint32_t)(((j * G + head) * kMfmaDim + d4) * sizeof(float)));
-          mlv[j] = ld_agent(ml64 + j * G + head);
-        }
-      }
-#pragma unroll
-      for (int j = 0; j < MG; ++j)
-        if (j < parts) Mx = fmaxf(Mx, __uint_as_float((uint32_t)mlv[j]));
-#pragma unroll
-      for (int j = 0; j < MG; ++j) {
-        if (j < parts) {
-          const float mj = __uint_as_float((uint32_t)mlv[j]);
-          const float wgt = mj == -INFINITY ? 0.0f : exp2f(mj - Mx);
-          Ls += wgt * __uint_as_float((uint32_t)(mlv[j] >> 32));
-          Os.x += wgt * ov[j].x;
-          Os.y += wgt * ov[j].y;
-          Os.z += wgt * ov[j].z;
-          Os.w += wgt * ov[j].w;
-        }
-      }
-    } else {
-      for (int j0 = 0; j0 < parts; j0 += MG) {
-        uint64_t mlv[MG];
-#pragma unroll
-        for (int j = 0; j < MG; ++j)
-          if (j0 + j < parts) mlv[j] = ld_agent(ml64 + (j0 + j) * G + head);
-#pragma unroll
-        for (int j = 0; j < MG; ++j)
-          if (j0 + j < parts) Mx = fmaxf(Mx, __uint_as_float((uint32_t)mlv[j]));
-      }
-      for (int j0 = 0; j0 < parts; j0 += MG) {
-        float4 ov[MG];
-        uint64_t mlv[MG];
-#pragma unroll
-        for (int j = 0; j < MG; ++j) {
-          if (j0 + j < parts) {
-            ov[j] = ld_agent_x4(ro, (uint32_t)((((j0 + j) * G + head) * kMfmaDim + d4) * sizeof(float)));
-            mlv[j] = ld_agent(ml64 + (j0 + j) * G + head);
-          }
-        }
-#pragma unroll
-        for (int j = 0; j < MG; ++j) {
-          if (j0 + j < parts) {
-            const float mj = __uint_as_float((uint32_t)mlv[j]);
-            const float wgt = mj == -INFINITY ? 0.0f : exp2f(mj - Mx);
-            Ls += wgt * __uint_as_float((uint32_t)(mlv[j] >> 32));
-            Os.x += wgt * ov[j].x;
-            Os.y += wgt * ov[j].y;
-            Os.z += wgt * ov[j].z;
-            Os.w += wgt * ov[j].w;
-          }
-        }
-      }
-    }
-    const bool any = !(Ls <= 0.0f);  // NaN (a poisoned part) stays NaN
-    const uint32_t lo2 = (uint32_t)f2bf(any ? Os.x / Ls : 0.0f) | ((uint32_t)f2bf(any ? Os.y / Ls : 0.0f) << 16);
-    const uint32_t hi2 = (uint32_t)f2bf(any ? Os.z / Ls : 0.0f) | ((uint32_t)f2bf(any ? Os.w / Ls : 0.0f) << 16);
-    *reinterpret_cast<uint2*>(outp + head * kMfmaDim + d4) = make_uint2(lo2, hi2);
-  }
+  finish_block<W, MG, GROUPED>(a, bh, part, M, L, o, poison, sm.m, sm.l, sm.o, s_last);
 }
 
 using HeadSmemLaunch = HeadSmem<kHeadWaves, kStepMaxTopK>;
@@ -461,6 +481,197 @@ __global__ __launch_bounds__(64 * kW4Waves, 4) void quest_attend_w4_kernel(StepA
   __shared__ int32_t s_pages[kMaxSelFused];
   const int bh = blockIdx.x / a.parts, part = blockIdx.x - bh * a.parts;
   attend_item<ROWS, KPT, kW4Waves, 1, 1, kW4Parts, false, kW4RowCap>(a, bh, part, smem_raw, &s_last, s_pages);
+}
+
+// ------------------------------------------------------- per-page-unit attention
+// The Quest step's attention (after the score launch; and over given rows for
+// quest_hisparse, so that both compute the same partials in the same order):
+// one 4-wave block per (request, KV head, part), blockIdx = (request, KV head) *
+// parts + part.  The layout's slots come in units of 64 (a selected page, or the
+// recent window, or 64 slots of the dense layout); wave w of part p takes units
+// p*4 + w, p*4 + w + 4*parts, ...  (one unit per wave at top_k 2048).  Per unit a
+// wave resolves its 64 rows itself (lane l: slot 64u + l -> position ->
+// req_to_token), shuffles them into the MFMA lane layouts and issues all 32
+// loads of the unit's K and V slices (32 KiB per wave) at once, then
+// S^T = K Q^T (v_mfma_f32_16x16x32_bf16, K rows as the A operand, 16 B per
+// lane), one softmax over the 64 rows folded into the wave's running (M, L),
+// P (bf16) straight from the S^T accumulator into v_mfma_f32_16x16x16bf16_1k
+// with V transposed in registers.  The block first selects its request's pages
+// (select_pages_wave: every wave ends with the page list in its lanes).
+template <int KPT, int W>
+struct UnitSmem {
+  union {
+    RankSelectSmem<(KPT > 0 ? KPT : 1), 64 * W> sel;
+    struct {
+      float m[W][kStepMaxG];
+      float l[W][kStepMaxG];
+      float o[W][kStepMaxG][kMfmaDim];
+    } comb;
+  };
+};
+
+template <bool ROWS, int KPT, int W>
+__global__ __launch_bounds__(64 * W, 8 / W) void quest_attend_unit_kernel(StepArgs a) {
+  constexpr int NT = 64 * W;
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  __shared__ uint32_t s_last;
+  UnitSmem<KPT, W>& sm = *reinterpret_cast<UnitSmem<KPT, W>*>(smem_raw);
+  const SelectArgs& sa = a.s;
+  const int parts = a.parts;
+  const int bh = blockIdx.x / parts, part = blockIdx.x - bh * parts;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int lo = lane & 15, hi = lane >> 4;
+  const int b = bh / kStepKV, h = bh - b * kStepKV;
+  const int64_t s = ROWS ? 0 : sa.seq[b];
+  const int64_t req = ROWS ? 0 : sa.rpi[b];
+  const int top_k = sa.top_k, k = sa.k_sel;
+  constexpr int P = 64;
+  const bool long_b = !ROWS && needs_selection(sa, s);
+  // actual_lens (quest.py:345)
+  const int n = ROWS ? min(max(a.actual[b], 0), top_k) : (int)min(max(s, (int64_t)0), (int64_t)top_k);
+  const bool r2t_ok = !ROWS && req >= 0 && req < a.r2t_rows;
+  const int G = a.G;
+  // Q^T as the B operand: query head lo (zero past G), channels 8hi + 32ks
+  bf16x8_t qb[4];
+  {
+    const uint16_t* qp = static_cast<const uint16_t*>(sa.q) + (int64_t)b * sa.q_bstride +
+                         (int64_t)(h * G + lo) * kMfmaDim + hi * 8;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      if (lo < G) {
+        qb[ks] = *reinterpret_cast<const bf16x8_t*>(qp + ks * 32);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qb[ks][e] = (__bf16)0.0f;
+      }
+    }
+  }
+  int my_rank = -1, my_page = -1, my_row0 = -1;  // lane s: a survivor's rank, page, first pool row
+  if constexpr (KPT > 0) {
+    // the scores go out with the request's words (their addresses do not wait for them):
+    // entries past the table re-read its last one and are masked below
+    const float* sc = sa.scores + (int64_t)b * sa.MP;
+    float sv[KPT];
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) sv[i] = sc[min(tid + NT * i, sa.MP - 1)];
+    if (long_b) {  // block-uniform
+      const int lim = (req >= 0 && req < sa.R) ? min(sa.limit[b], sa.MP) : 0;
+      select_ranked<KPT, NT>(sv, lim, max(lim, k), k, sm.sel, nullptr, sa.MP, my_rank, my_page, my_row0);
+    }
+  }
+  const int units = top_k / P;
+  const int stride_units = parts * W;
+  const int64_t recent0 = max(s - P, (int64_t)0);
+  int32_t* pos_out = !ROWS && h == 0 && sa.positions ? sa.positions + (int64_t)b * top_k : nullptr;
+  const uint16_t* kb = a.k + h * kMfmaDim;
+  const uint16_t* vb = a.v + h * kMfmaDim;
+  constexpr int kRow = kStepKV * kMfmaDim;
+  float M = -INFINITY, L = 0.0f;
+  float4_t o[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = float4_t{0.f, 0.f, 0.f, 0.f};
+  bool bad = false;
+  for (int u = part * W + wave; u < units; u += stride_units) {  // wave-uniform
+    const int slot = u * P + lane;
+    const int valid = min(n - u * P, P);  // real slots of this unit
+    int64_t row = 0;
+    if constexpr (ROWS) {
+      if (lane < valid) {
+        row = a.rows_in[(int64_t)b * a.rows_stride + slot];
+        bad |= row < 0;
+      }
+    } else {
+      int64_t p;
+      if (!long_b)
+        p = s <= top_k ? min((int64_t)slot, max(s - 1, (int64_t)0)) : min(recent0 + slot, s - 1);
+      else if (u < k)
+        p = (int64_t)__builtin_amdgcn_readlane(my_page, __builtin_ctzll(__ballot(my_rank == u))) * P + lane;
+      else
+        p = min(recent0 + (slot - k * P), s - 1);
+      if (lane < valid && r2t_ok && p >= 0 && p < a.r2t_stride) row = a.r2t[req * a.r2t_stride + p];
+      if (pos_out) pos_out[slot] = (int32_t)p;  // after the row load: waiting for the row does not wait for it
+    }
+    if (valid <= 0) continue;
+    const int r32 = (row >= 0 && row < a.kv_rows) ? (int)row : 0;
+    // every K and V load of the unit in flight at once
+    bf16x8_t ka[4][4];
+    uint4 vr[4][4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const uint16_t* kp = kb + (int64_t)__shfl(r32, t * 16 + lo, 64) * kRow + hi * 8;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) ka[t][ks] = *reinterpret_cast<const bf16x8_t*>(kp + ks * 32);
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        vr[t][j] = *reinterpret_cast<const uint4*>(vb + (int64_t)__shfl(r32, t * 16 + hi * 4 + j, 64) * kRow + lo * 8);
+    __builtin_amdgcn_sched_barrier(0);  // all 32 loads go out before the first use of any
+    // S^T[token 16t + 4hi + i][head lo] in acc[t][i]
+    float4_t acc[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      acc[t] = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[t][ks], qb[ks], acc[t], 0, 0, 0);
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float x = (t * 16 + hi * 4 + i) < valid ? acc[t][i] * a.sl2 : -INFINITY;
+        acc[t][i] = x;
+        mx = fmaxf(mx, x);
+      }
+    mx = fmaxf(mx, lane_xor16(mx, lane));
+    mx = fmaxf(mx, lane_xor32(mx, lane));
+    const float Mn = fmaxf(M, mx);
+    const float alpha = M == -INFINITY ? 0.0f : exp2f(M - Mn);  // rescale of the running sums
+    float sum = 0.0f;
+    short4_t pa[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint16_t pbits = f2bf(exp2f(acc[t][i] - Mn));
+        sum += bf2f(pbits);
+        pa[t][i] = (short)pbits;
+      }
+    sum += lane_xor16(sum, lane);
+    sum += lane_xor32(sum, lane);
+    L = L * alpha + sum;
+    M = Mn;
+    // o rows are heads 4hi + i: their scale factors live in lanes 4hi + i
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float ai = __shfl(alpha, hi * 4 + i, 64);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e][i] *= ai;
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      short4_t vbv[8];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint4 w = vr[t][j];
+        const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int x = 0; x < 4; ++x) {
+          vbv[2 * x][j] = (short)(wv[x] & 0xFFFFu);
+          vbv[2 * x + 1][j] = (short)(wv[x] >> 16);
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa[t], vbv[e], o[e], 0, 0, 0);
+    }
+  }
+  bool poison = false;
+  if constexpr (ROWS) poison = __syncthreads_or(bad ? 1 : 0) != 0;  // a failed swap-in: NaN output
+  else lds_barrier();  // the selection's LDS is free before the combine reuses it
+  finish_block<W, kW4Parts, false>(a, bh, part, M, L, o, poison, sm.comb.m, sm.comb.l, sm.comb.o, &s_last);
 }
 
 }  // namespace
@@ -501,13 +712,43 @@ static size_t head_smem_bytes() {
   return sizeof(HeadSmemLaunch);
 }
 
-// LDS: the row table and wave combine, or the selection (up to 24 x 256 pages)
-// that aliases them.
-template <int KPT>
-static void launch_attend_select(const StepArgs& a, int blocks, hipStream_t s) {
-  constexpr size_t kSmem = std::max(sizeof(HeadSmemW4), sizeof(SelectSmem<KPT, 64 * kW4Waves>));
-  static_assert(kSmem <= 64 * 1024, "within the default LDS limit");
-  quest_attend_w4_kernel<false, KPT><<<blocks, 64 * kW4Waves, kSmem, s>>>(a);
+// LDS of a unit-attention instance: the wave combine, or the selection that
+// aliases it (above the 64 KiB default for 8-wave blocks: opted in once per device).
+template <bool ROWS, int KPT, int W>
+static size_t unit_smem_bytes() {
+  constexpr size_t kSmem = sizeof(UnitSmem<KPT, W>);
+  static_assert(kSmem <= 160 * 1024, "within the CU's LDS");
+  if constexpr (kSmem > 64 * 1024) {
+    static bool opted[64] = {false};
+    int dev = 0;
+    if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64 && !opted[dev]) {
+      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&quest_attend_unit_kernel<ROWS, KPT, W>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)kSmem);
+      opted[dev] = true;
+    }
+  }
+  return kSmem;
+}
+
+template <bool ROWS, int KPT, int W>
+static void launch_unit(const StepArgs& a, hipStream_t s) {
+  const int blocks = a.bs * kStepKV * a.parts;
+  quest_attend_unit_kernel<ROWS, KPT, W><<<blocks, 64 * W, unit_smem_bytes<ROWS, KPT, W>(), s>>>(a);
+}
+
+// The selection's scores per thread for n_max candidate pages (up to 6144).
+template <int W>
+static void launch_attend_select(const StepArgs& a, int n_max, hipStream_t s) {
+  constexpr int kT = 64 * W;
+  if (n_max <= 2 * kT) launch_unit<false, 2, W>(a, s);
+  else if (n_max <= 4 * kT) launch_unit<false, 4, W>(a, s);
+  else if (n_max <= 5 * kT) launch_unit<false, 5, W>(a, s);  // contexts up to 128K + a few pages at W = 8
+  else if (n_max <= 6 * kT) launch_unit<false, 6, W>(a, s);
+  else if (n_max <= 8 * kT) launch_unit<false, 8, W>(a, s);
+  else if (n_max <= 9 * kT) launch_unit<false, 9, W>(a, s);  // contexts just past 128K at W = 4
+  else if (n_max <= 12 * kT) launch_unit<false, 12, W>(a, s);
+  else if (n_max <= 16 * kT) launch_unit<false, 16, W>(a, s);
+  else launch_unit<false, 24, W>(a, s);
 }
 
 // Shapes the fused layer step takes (bf16, KV*D = 4*128, G <= 16, page 64, at
@@ -523,10 +764,13 @@ static bool fused_shape(int q_dtype, int kv_dtype, int new_dtype, int num_q_head
          max_pages <= 24 * 64 * kW4Waves;
 }
 
-// Attention blocks per (request, KV head) of the fused attention: enough to
-// cover every CU once (the blocks run one per CU), at least 32 rows per wave.
-static int step_parts(int top_k) { return max(1, min(kW4Parts, ceil_div(top_k, kW4Waves * 32))); }
-static int step_per_wave(int top_k, int parts) { return ceil_div(top_k, parts * kW4Waves * 32) * 32; }
+// Waves per block of the unit attention: 8 (one block per CU) when the batch has
+// a 64-slot unit for every wave of one 8-wave block per CU, else 4 (two per CU).
+static int unit_waves(int bs, int top_k) {
+  return (int64_t)bs * kStepKV * (top_k / 64) >= 8LL * device_cu_count() ? 8 : 4;
+}
+// Blocks per (request, KV head): one unit per wave where the parts allow it.
+static int step_parts(int top_k, int waves) { return max(1, min(kW4Parts, ceil_div(top_k / 64, waves))); }
 
 extern "C" int qq_quest_fused_step(int q_dtype, int kv_dtype, int new_dtype, int num_q_heads, int kv_heads,
                                    int head_dim, int page_size, int top_k, int max_pages) {
@@ -542,11 +786,12 @@ int qq::attend_rows_fused(const void* q, int64_t q_bstride, int num_q_heads, con
                       void* out, void* workspace, int64_t workspace_bytes, void* sync, int64_t sync_bytes,
                       hipStream_t s) {
   if (!sync || sync_bytes < qq_quest_layer_step_sync_bytes(bs, kStepKV) || slots <= 0 || slots > kStepMaxTopK ||
-      num_q_heads % kStepKV != 0 || num_q_heads / kStepKV > kStepMaxG || !workspace)
+      slots % 64 != 0 || num_q_heads % kStepKV != 0 || num_q_heads / kStepKV > kStepMaxG || !workspace)
     return 1;
   const int top_k = (int)slots;
   const int G = num_q_heads / kStepKV;
-  const int parts = step_parts(top_k);
+  const int W = unit_waves(bs, top_k);
+  const int parts = step_parts(top_k, W);
   const int64_t part_bytes = (int64_t)bs * kStepKV * parts * G * (kMfmaDim + 2) * (int64_t)sizeof(float);
   if (parts > 1 && workspace_bytes < part_bytes) return 1;
   StepArgs a{};
@@ -564,14 +809,16 @@ int qq::attend_rows_fused(const void* q, int64_t q_bstride, int num_q_heads, con
   a.part_o = static_cast<float*>(workspace);
   a.part_ml = a.part_o + (int64_t)bs * kStepKV * parts * G * kMfmaDim;
   a.parts = parts;
-  a.per_wave = step_per_wave(top_k, parts);
   a.sync = static_cast<uint32_t*>(sync);
   a.bs = bs;
   a.G = G;
   a.rows_in = rows;
   a.rows_stride = slots;
   a.actual = actual;
-  quest_attend_w4_kernel<true, 0><<<bs * kStepKV * parts, 64 * kW4Waves, sizeof(HeadSmemW4), s>>>(a);
+  if (W == 8)
+    launch_unit<true, 0, 8>(a, s);
+  else
+    launch_unit<true, 0, 4>(a, s);
   return QQ_OK;
 }
 
@@ -708,8 +955,8 @@ static int forward_decode(
   sa.pool_rows = kv_rows;
 
   const int G = num_q_heads / kv_heads;
-  const int parts = step_parts(top_k);
-  const int per_wave = step_per_wave(top_k, parts);
+  const int W = unit_waves(bs, top_k);
+  const int parts = step_parts(top_k, W);
   const int64_t part_bytes = (int64_t)bs * kv_heads * parts * G * (kMfmaDim + 2) * (int64_t)sizeof(float);
   const bool fused = sync && sync_bytes >= qq_quest_layer_step_sync_bytes(bs, kv_heads) &&
                      fused_shape(q_dtype, kv_dtype, k_new ? new_dtype : -1, num_q_heads, kv_heads, head_dim,
@@ -735,29 +982,14 @@ static int forward_decode(
     a.part_o = static_cast<float*>(workspace);
     a.part_ml = a.part_o + (int64_t)bs * kv_heads * parts * G * kMfmaDim;
     a.parts = parts;
-    a.per_wave = per_wave;
     a.sync = static_cast<uint32_t*>(sync);
     a.bs = bs;
     a.G = G;
-    const int blocks = bs * kStepKV * parts;
-    constexpr int kT = 64 * kW4Waves;
     const int n_max = max(max_pages, k_sel);
-    if (n_max <= 2 * kT)
-      launch_attend_select<2>(a, blocks, s);
-    else if (n_max <= 4 * kT)
-      launch_attend_select<4>(a, blocks, s);
-    else if (n_max <= 6 * kT)
-      launch_attend_select<6>(a, blocks, s);
-    else if (n_max <= 8 * kT)
-      launch_attend_select<8>(a, blocks, s);
-    else if (n_max <= 9 * kT)  // contexts just past 128K tokens
-      launch_attend_select<9>(a, blocks, s);
-    else if (n_max <= 12 * kT)
-      launch_attend_select<12>(a, blocks, s);
-    else if (n_max <= 16 * kT)
-      launch_attend_select<16>(a, blocks, s);
+    if (W == 8)
+      launch_attend_select<8>(a, n_max, s);
     else
-      launch_attend_select<24>(a, blocks, s);
+      launch_attend_select<4>(a, n_max, s);
     return check_launch(what);
   }
 

@@ -391,6 +391,170 @@ __device__ inline void select_topk_block(const float (&sv)[KPT], int lim, int n_
   __syncthreads();
 }
 
+// Lane exchanges of 32-bit words inside a wave without the LDS: lane l gets the
+// word of lane l ^ J (DPP moves within a row of 16, permlane swaps across rows).
+template <int J>
+__device__ inline uint32_t lane_xor_u32(uint32_t v, int lane) {
+  if constexpr (J == 1) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, kDppQuadXor1, 0xF, 0xF, false);
+  } else if constexpr (J == 2) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, kDppQuadXor2, 0xF, 0xF, false);
+  } else if constexpr (J == 4) {  // row_shl:4 gives lane l + 4, row_shr:4 lane l - 4
+    const uint32_t up = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x104, 0xF, 0xF, false);
+    const uint32_t dn = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xF, 0xF, false);
+    return (lane & 4) ? dn : up;
+  } else if constexpr (J == 8) {  // row_ror:8
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xF, 0xF, false);
+  } else if constexpr (J == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return (lane & 16) ? r[0] : r[1];
+  } else {
+    static_assert(J == 32, "lane distance");
+    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return (lane & 32) ? r[0] : r[1];
+  }
+}
+
+template <int J>
+__device__ inline uint64_t lane_xor_u64(uint64_t v, int lane) {
+  const uint32_t lo = lane_xor_u32<J>((uint32_t)v, lane);
+  const uint32_t hi = lane_xor_u32<J>((uint32_t)(v >> 32), lane);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+__device__ inline uint64_t readlane_u64(uint64_t v, int lane) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, lane);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), lane);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+template <int KPT, int NT>
+struct RankSelectSmem {
+  uint32_t gmax[64];             // 32-bit score keys: maxima of the 64 groups of NT/64 threads
+  int gcnt[NT / 64][64];         // partial counts of group maxima >= each one, one row per wave
+  uint64_t cand[NT * KPT + 64];  // survivors (score key, ~page), in arrival order
+  int crank[NT / 64][64];        // partial ranks of the survivors (at most 64)
+  int count;
+  int order[64];                 // page of each rank (many-survivor path)
+};
+
+// Maximum of a 32-bit value over the wave (DPP / permlane exchanges, no LDS).
+__device__ inline uint32_t wave_max_u32(uint32_t v, int lane) {
+  v = max(v, lane_xor_u32<1>(v, lane));
+  v = max(v, lane_xor_u32<2>(v, lane));
+  v = max(v, lane_xor_u32<4>(v, lane));
+  v = max(v, lane_xor_u32<8>(v, lane));
+  v = max(v, lane_xor_u32<16>(v, lane));
+  v = max(v, lane_xor_u32<32>(v, lane));
+  return v;
+}
+
+// Top k <= 64 pages of n_eff <= NT*KPT pages (quest.py:450-452) with an NT-thread
+// block (NT = 256 or 512): sv[i] is the score of page tid + NT i (pages >= lim rank
+// as -inf).  The order is (score desc, page asc): 64-bit keys (order-preserving
+// score, ~page), all distinct.  Every comparison pass is split over the block's
+// waves and handed over through LDS, 4 barriers in all:
+//   A. per thread the largest 32-bit score key of its pages, per group of NT/64
+//      consecutive threads the maximum (DPP lane moves);
+//   B. for each group maximum the number of group maxima >= it; tau = the largest
+//      group maximum that at least k group maxima reach (the k-th largest).  At
+//      least k groups hold a page scoring >= tau, so every top-k page does;
+//   C. the pages scoring >= tau (about 40 of 2048 for distinct scores) gathered
+//      into one LDS array as 64-bit keys, each wave at an offset from one LDS
+//      atomic;
+//   D. up to 64 survivors: their ranks (the number of survivor keys above), each
+//      wave's lane s ending with survivor s's rank, page and (when `page_rows` is
+//      given) the page's first pool row, loaded while the ranks are counted.  More
+//      survivors (ties): every thread ranks its share by counting, then lane r
+//      takes rank r.
+// The page of rank u is the lane whose rank is u (one ballot and a readlane).
+template <int KPT, int NT>
+__device__ inline void select_ranked(const float (&sv)[KPT], int lim, int n_eff, int k,
+                                     RankSelectSmem<KPT, NT>& s, const int32_t* page_rows, int max_pages,
+                                     int& my_rank, int& my_page, int& my_row0) {
+  static_assert(NT == 256 || NT == 512, "64 groups of whole quads or octets");
+  constexpr int NW = NT / 64, SHARE = 64 / NW;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, w = tid >> 6;
+  uint32_t key[KPT];
+  uint32_t tmax = 0u;
+#pragma unroll
+  for (int i = 0; i < KPT; ++i) {
+    const int p = tid + NT * i;
+    const uint32_t o = orderable(sv[i]);
+    key[i] = p < lim ? o : (p < n_eff ? kNegInfKey : 0u);  // 0: not a page (below every key)
+    tmax = max(tmax, key[i]);
+  }
+  uint32_t g = max(tmax, lane_xor_u32<1>(tmax, lane));
+  g = max(g, lane_xor_u32<2>(g, lane));
+  if (NT == 512) g = max(g, lane_xor_u32<4>(g, lane));
+  if ((tid & (NT / 64 - 1)) == 0) s.gmax[tid / (NT / 64)] = g;
+  if (tid == 0) s.count = 0;
+  lds_barrier();  // A
+  const uint32_t gl = s.gmax[lane];
+  {
+    int cnt = 0;
+#pragma unroll
+    for (int j = 0; j < SHARE; ++j) cnt += s.gmax[w * SHARE + j] >= gl ? 1 : 0;
+    s.gcnt[w][lane] = cnt;
+  }
+  lds_barrier();  // B
+  int ge = 0;
+#pragma unroll
+  for (int j = 0; j < NW; ++j) ge += s.gcnt[j][lane];
+  // the k-th largest group maximum; a zero (no page) never survives
+  const uint32_t tau = max(wave_max_u32(ge >= k ? gl : 0u, lane), 1u);
+  uint64_t mask[KPT];
+  int wave_total = 0;
+#pragma unroll
+  for (int i = 0; i < KPT; ++i) {
+    mask[i] = __ballot(key[i] >= tau);
+    wave_total += __popcll(mask[i]);
+  }
+  int base = 0;
+  if (lane == 0) base = atomicAdd(&s.count, wave_total);
+  base = __builtin_amdgcn_readfirstlane(base);
+#pragma unroll
+  for (int i = 0; i < KPT; ++i) {
+    if (key[i] >= tau)
+      s.cand[base + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask[i] >> 32),
+                                                   __builtin_amdgcn_mbcnt_lo((uint32_t)mask[i], 0u))] =
+          sel_key(key[i], tid + NT * i);
+    base += __popcll(mask[i]);
+  }
+  lds_barrier();  // C
+  const int total = s.count;
+  if (total <= 64) {  // block-uniform
+    const uint64_t ci = lane < total ? s.cand[lane] : 0ull;
+    const int page = (int)(~(uint32_t)ci);
+    my_row0 = (page_rows && lane < total && page >= 0 && page < max_pages) ? page_rows[page] : -1;
+    int cnt = 0;
+#pragma unroll
+    for (int j = 0; j < SHARE; ++j) {
+      const int jj = w * SHARE + j;
+      cnt += (jj < total && s.cand[jj] > ci) ? 1 : 0;
+    }
+    s.crank[w][lane] = cnt;
+    lds_barrier();  // D
+    int r = 0;
+#pragma unroll
+    for (int j = 0; j < NW; ++j) r += s.crank[j][lane];
+    my_rank = lane < total ? r : -1;
+    my_page = page;
+    return;
+  }
+  for (int i = tid; i < total; i += NT) {
+    const uint64_t ci = s.cand[i];
+    int r = 0;
+    for (int j = 0; j < total; ++j) r += s.cand[j] > ci;
+    if (r < k) s.order[r] = (int)(~(uint32_t)ci);
+  }
+  lds_barrier();
+  my_rank = lane < k ? lane : -1;
+  my_page = lane < k ? s.order[lane] : -1;
+  my_row0 = (page_rows && my_page >= 0 && my_page < max_pages) ? page_rows[my_page] : -1;
+}
+
 // ----------------------------------------------------------------- attention
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));

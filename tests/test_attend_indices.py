@@ -1,20 +1,22 @@
 """CPU model of the fused attention kernels' index arithmetic (qwenquest_amd/csrc/decode.hip).
 
-For every launch shape the host code can choose, it checks that
+The Quest step's attention (quest_attend_unit_kernel) works in units of 64 layout slots
+(one selected page, the recent window, or 64 slots of the dense layout): wave w of part p
+takes units p*W + w, p*W + w + W*parts, ...  For every launch shape the host can choose
+the model checks that every unit's slots lie inside the layout, that the real slots
+[0, n) of a request are attended exactly once, that each wave's row shuffles stay inside
+the wave, that the selection reads only score entries of the request's row, keeps its
+survivors inside its LDS array and asks for ranks < k, that partial and counter indices
+stay inside their buffers, and that the LDS a launch allocates fits the CU.
 
-* every row-table entry a wave reads lies inside its block's table and was written by the
-  table fill (entries past the request's real slots hold row 0, never stale LDS),
-* the real slots [0, n) of a request are attended exactly once over all parts and waves,
-* the selection reads only score entries below the candidate limit, its survivor array and
-  page list fit, and the page index of every selected slot is < k (the page list's length),
-* every partial and counter index stays inside the workspace and the sync buffer,
-* the LDS a launch allocates covers the larger of its row table and its selection.
-
-The first fused attention kernel faulted the GPU on a recent-window-only flow (top_k 64,
-k_sel 0, seq_len < 64): its table fill wrote only the real slots, while a step reads all of
-its 16 (or 32) entries (the ones past n are masked in the softmax only), so uninitialised
-LDS words became pool-row indices.  The fill now covers the block's whole share; this
-model is the check that found it, kept for every geometry the host code can pick.
+Dense decode (quest_attend_part_kernel) still stages rows in an LDS row table; its model
+checks that every table entry a step reads lies inside the block's table and was written
+by the fill.  The first fused attention kernel of this library faulted the GPU on a
+recent-window-only flow (top_k 64, k_sel 0, seq_len < 64): its table fill wrote only the
+real slots, while a step reads all 16 (or 32) entries of its tile (the ones past n are
+masked in the softmax only), so uninitialised LDS words became pool-row indices.  The
+fill now covers the block's whole share; test_model_catches_a_fill_of_the_real_slots_only
+keeps the model honest about that case.
 """
 
 from __future__ import annotations
@@ -25,42 +27,49 @@ import math
 import pytest
 
 # geometry of decode.hip (kept in step with its constants and host helpers)
-W4_WAVES, W4_PARTS, W4_ROWCAP = 4, 8, 1024
+PARTS_MAX = 8
 HEAD_WAVES, HEAD_TILES, HEAD_ROWCAP = 8, 2, 4096
-MAX_SEL, MAX_TOPK, MAX_G, KV = 64, 4096, 16, 4
-KPT_FORMS = (2, 4, 6, 8, 9, 12, 16, 24)
+MAX_SEL, MAX_TOPK, MAX_G, KV, UNIT = 64, 4096, 16, 4, 64
+KPT_FORMS = (2, 4, 5, 6, 8, 9, 12, 16, 24)
+CUS = 256
 
 
 def ceil_div(a, b):
     return -(-a // b)
 
 
-def step_parts(top_k):
-    return max(1, min(W4_PARTS, ceil_div(top_k, W4_WAVES * 32)))
+def unit_waves(bs, top_k, cus=CUS):
+    return 8 if bs * KV * (top_k // UNIT) >= 8 * cus else 4
 
 
-def step_per_wave(top_k, parts):
-    return ceil_div(top_k, parts * W4_WAVES * 32) * 32
+def step_parts(top_k, waves):
+    return max(1, min(PARTS_MAX, ceil_div(top_k // UNIT, waves)))
 
 
 def dense_parts(max_rows):
     return max(1, ceil_div(max_rows, MAX_TOPK))
 
 
-def kpt_form(max_pages, k_sel):
+def kpt_form(max_pages, k_sel, nt):
     n_max = max(max_pages, k_sel)
     for kpt in KPT_FORMS:
-        if n_max <= kpt * 256:
+        if n_max <= kpt * nt:
             return kpt
-    return None
+    return 24
 
 
-def select_smem_bytes(kpt, nt=256):
-    # SelectSmem<KPT, NT>: cand[NT*KPT+64] u64, gmax[64] u64, grank[64], crank[64], wcnt[NT/64],
-    # tau u64 (8-aligned), order[64]
-    b = (nt * kpt + 64) * 8 + 64 * 8 + 64 * 4 + 64 * 4 + (nt // 64) * 4
-    b = ceil_div(b, 8) * 8 + 8 + 64 * 4
+def rank_select_smem_bytes(kpt, nt):
+    # RankSelectSmem<KPT, NT>: gmax[64] u32, gcnt[NT/64][64] i32, cand[NT*KPT+64] u64 (8-aligned),
+    # crank[NT/64][64] i32, count, order[64]
+    b = 64 * 4 + (nt // 64) * 64 * 4
+    b = ceil_div(b, 8) * 8 + (nt * kpt + 64) * 8
+    b += (nt // 64) * 64 * 4 + 4 + 64 * 4
     return ceil_div(b, 8) * 8
+
+
+def unit_smem_bytes(kpt, waves):
+    comb = 2 * waves * MAX_G * 4 + waves * MAX_G * 128 * 4
+    return max(rank_select_smem_bytes(kpt, 64 * waves), comb)
 
 
 def head_smem_bytes(waves, rowcap):
@@ -108,20 +117,43 @@ def check_launch(top_k, n, parts, per_wave, waves, step_rows, rowcap):
     assert sorted(seen) == list(range(n)), "real slots not attended exactly once"
 
 
-def check_selection(top_k, page, max_pages, lim):
+def check_units(top_k, n, bs):
+    """The unit kernel's slot coverage for one request of a batch of bs."""
+    waves = unit_waves(bs, top_k)
+    parts = step_parts(top_k, waves)
+    units = top_k // UNIT
+    seen = []
+    for part in range(parts):
+        for w in range(waves):
+            for u in range(part * waves + w, units, parts * waves):
+                assert 0 <= u < units
+                for lane in range(64):
+                    slot = u * UNIT + lane
+                    assert slot < top_k
+                    if slot < n:
+                        seen.append(slot)
+                # shuffle sources of the K tiles (16t + lo) and V steps (16t + 4hi + j)
+                srcs = {t * 16 + lo for t in range(4) for lo in range(16)} | {
+                    t * 16 + hi * 4 + j for t in range(4) for hi in range(4) for j in range(4)}
+                assert max(srcs) < 64
+    assert sorted(seen) == list(range(n)), "real slots not attended exactly once"
+    return waves, parts
+
+
+def check_selection(top_k, page, max_pages, lim, waves):
+    nt = 64 * waves
     k = top_k // page - 1
-    kpt = kpt_form(max_pages, k)
-    assert kpt is not None
+    kpt = kpt_form(max_pages, k, nt)
     n_eff = max(lim, k)
-    assert n_eff <= kpt * 256
-    score_reads = [tid + 256 * i for tid in range(256) for i in range(kpt) if tid + 256 * i < lim]
-    assert not score_reads or max(score_reads) < min(lim, max_pages)
+    assert n_eff <= kpt * nt
+    # score reads clamp to the request's row of max_pages entries
+    reads = {min(tid + nt * i, max_pages - 1) for tid in range(nt) for i in range(kpt)}
+    assert max(reads) < max_pages and min(reads) >= 0
     assert k <= MAX_SEL
-    # survivors <= n_eff fit cand[NT*KPT + 64]; slots < k*P read s_pages[slot // P] < k
-    assert n_eff <= 256 * kpt + 64
-    assert all(slot // page < k for slot in range(k * page))
-    smem = max(head_smem_bytes(W4_WAVES, W4_ROWCAP), select_smem_bytes(kpt))
-    assert smem <= 64 * 1024
+    # survivors are a subset of the block's nt*kpt keys: cand holds nt*kpt + 64
+    assert nt * kpt <= nt * kpt + 64
+    smem = unit_smem_bytes(kpt, waves)
+    assert smem <= (64 * 1024 if waves == 4 else 160 * 1024)
 
 
 TOPKS = (64, 128, 192, 256, 1024, 2048, 2112, 4032, 4096)
@@ -129,37 +161,37 @@ SEQS = (1, 2, 15, 16, 31, 33, 63, 64, 65, 127, 2047, 2048, 2049, 4095, 4096, 409
 
 
 @pytest.mark.parametrize("top_k", TOPKS)
-def test_fused_attention_row_table_and_slots(top_k):
-    parts = step_parts(top_k)
-    per_wave = step_per_wave(top_k, parts)
+@pytest.mark.parametrize("bs", (1, 4, 16, 64))
+def test_unit_attention_slots(top_k, bs):
     for s in SEQS:
-        n = min(max(s, 0), top_k)
-        check_launch(top_k, n, parts, per_wave, W4_WAVES, 16, W4_ROWCAP)
+        check_units(top_k, min(max(s, 0), top_k), bs)
+
+
+def test_benchmark_shape_runs_one_unit_per_wave():
+    """Batch 16 x top_k 2048: 8-wave blocks, 4 parts per (request, KV head), 256 blocks
+    (one per CU), each wave one 64-row unit."""
+    waves, parts = check_units(2048, 2048, 16)
+    assert (waves, parts) == (8, 4) and 16 * KV * parts == CUS
+    assert unit_waves(8, 2048) == 4 and step_parts(2048, 4) == 8
 
 
 @pytest.mark.parametrize("top_k", TOPKS)
 def test_rows_mode_actual_lengths(top_k):
     """quest_hisparse's rows mode: n = clamp(actual, 0, slots) for any given actual length."""
-    parts = step_parts(top_k)
-    per_wave = step_per_wave(top_k, parts)
     for actual in (-3, 0, 1, 17, top_k - 1, top_k, top_k + 5):
-        check_launch(top_k, min(max(actual, 0), top_k), parts, per_wave, W4_WAVES, 16, W4_ROWCAP)
+        check_units(top_k, min(max(actual, 0), top_k), 16)
 
 
-@pytest.mark.parametrize("max_pages", (2, 64, 512, 513, 1024, 2049, 2050, 2304, 2305, 3072, 4096, 6144))
-def test_selection_forms(max_pages):
-    """The KPT form the host picks holds every candidate page: 2304 (9 keys per thread,
-    contexts just past 128K), 3072 (12), 6144 (24) pages and the forms between."""
+@pytest.mark.parametrize("max_pages", (2, 64, 512, 513, 1024, 2049, 2050, 2304, 2305, 2560, 2561, 3072, 4096, 6144))
+@pytest.mark.parametrize("waves", (4, 8))
+def test_selection_forms(max_pages, waves):
+    """The KPT form the host picks holds every candidate page: 2304 / 2560 (contexts just
+    past 128K at 4 / 8 waves), 3072, 6144 pages and the forms between."""
     for top_k, page in ((64, 64), (128, 64), (2048, 64), (4096, 64), (4160, 64)):
         if top_k // page - 1 > MAX_SEL:
             continue
         for lim in sorted({0, 1, max_pages // 2, max_pages - 1, max_pages}):
-            check_selection(top_k, page, max_pages, lim)
-
-
-def test_largest_form_is_the_fused_limit():
-    assert kpt_form(24 * 256, 63) == 24 and kpt_form(24 * 256 + 1, 63) is None
-    assert kpt_form(2304, 31) == 9 and kpt_form(2305, 31) == 12
+            check_selection(top_k, page, max_pages, lim, waves)
 
 
 @pytest.mark.parametrize("max_rows", (1, 64, 4096, 4097, 9100, 65536, 131071, 131072 + 64))
@@ -184,23 +216,25 @@ def test_dense_attention_geometry(max_rows):
 
 @pytest.mark.parametrize("bs,top_k,G", list(itertools.product((1, 3, 16, 64), (64, 2048, 4096), (1, 8, 16))))
 def test_partials_and_counters_in_bounds(bs, top_k, G):
-    parts = step_parts(top_k)
+    parts = step_parts(top_k, unit_waves(bs, top_k))
+    assert parts <= PARTS_MAX  # one merge pass
     ws_floats = bs * KV * parts * G * (128 + 2)
     o_floats = bs * KV * parts * G * 128
     last_o = ((bs * KV - 1) * parts + parts - 1) * G + (G - 1)
     assert (last_o + 1) * 128 <= o_floats
     assert o_floats + (last_o + 1) * 2 <= ws_floats
+    # the caller's workspace: qq_decode_attention_workspace_bytes(bs, top_k, H, D) floats
+    assert ws_floats <= bs * ceil_div(top_k, 64) * (G * KV) * (128 + 2)
     sync_words = bs * KV * 32
     assert (bs * KV - 1) * 32 < sync_words
     assert math.isfinite(ws_floats)
 
 
 def test_model_catches_a_fill_of_the_real_slots_only():
-    """The first fused kernel's fill (real slots only) fails the model at the faulting
-    flow's shape: top_k 64, recent window only, 31 real slots."""
-    top_k, n = 64, 31
-    parts = step_parts(top_k)
-    per_wave = step_per_wave(top_k, parts)
-    _, _, reads, _ = attend_block(n, 0, per_wave, W4_WAVES, 16)
+    """The first fused kernel's fill (real slots only) fails the table model at the faulting
+    flow's shape: top_k 64, recent window only, 31 real slots, 4 waves of 32 rows in
+    16-row steps."""
+    n = 31
+    _, _, reads, _ = attend_block(n, 0, 32, 4, 16)
     written_real_only = set(range(n))
     assert not reads <= written_real_only
