@@ -525,7 +525,7 @@ def main() -> int:
     ms_att = time_graph(attend, L, stream)
     bw_sel = byts["bounds"] / (ms_sel * 1e-3) / 1e9
     bw_att = byts["kv"] / (ms_att * 1e-3) / 1e9
-    dominant = ("quest_attend_w4_kernel", ms_att, byts["kv"], bw_att) if ms_att >= ms_sel else (
+    dominant = ("quest_attend_unit_kernel", ms_att, byts["kv"], bw_att) if ms_att >= ms_sel else (
         "score_pages_fast_kernel", ms_sel, byts["bounds"], bw_sel)
 
     cpu = None
@@ -567,7 +567,7 @@ def main() -> int:
         "tokens_per_s": round(B / (ms_per_step * 1e-3), 1),
         "algorithmic_bytes_per_layer_step": byts,
         "kernels_us": {"score_pages_fast_kernel": round(ms_sel * 1e3, 2),
-                       "quest_attend_w4_kernel": round(ms_att * 1e3, 2)},
+                       "quest_attend_unit_kernel": round(ms_att * 1e3, 2)},
         "roofline": {"kernel": dominant[0], "bound": "hbm", "achieved": round(dominant[3], 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(dominant[3] / HBM_PEAK_GBS, 4),
                      "traffic": None if args.ragged else traffic.get(dominant[0]),

@@ -44,14 +44,11 @@ constexpr int kHeadWaves = 8;        // dense decode: 8-wave blocks (two waves p
 constexpr int kHeadTiles = 2;        // 16-row tiles per step (32 rows)
 constexpr int kHeadDepth = 2;        // steps in flight per wave
 constexpr int kMaxParts = 8;         // dense decode: parts merged in one pass
-// The Quest step's attention: 4-wave blocks (at most 128 VGPRs, four per CU),
-// up to kW4Parts per (request, KV head); a wave streams 16-row steps one at a
-// time and a block's row table holds up to kW4RowCap slots (top_k <= 4096
-// needs at most 512).
-constexpr int kW4Waves = 4;
-constexpr int kW4Parts = 8;
-constexpr int kW4RowCap = 1024;
-constexpr int kUnitWaves = 4;
+// The Quest step's attention (quest_attend_unit_kernel): up to kUnitParts blocks
+// per (request, KV head), merged in one pass; the selection of a 4-wave block
+// holds up to 24 scores per thread (6144 pages).
+constexpr int kUnitParts = 8;
+constexpr int kUnitMinWaves = 4;
 
 struct StepArgs {
   SelectArgs s;            // scoring, selection, positions, new token
@@ -455,7 +452,6 @@ __device__ inline void attend_item(const StepArgs& a, int bh, int part, unsigned
 }
 
 using HeadSmemLaunch = HeadSmem<kHeadWaves, kStepMaxTopK>;
-using HeadSmemW4 = HeadSmem<kW4Waves, kW4RowCap>;
 
 // The attention launch of the fused layer step (and of the dense decode and
 // the attention over given rows): one 8-wave block per (request, KV head,
@@ -468,19 +464,6 @@ __global__ __launch_bounds__(64 * kHeadWaves, 1) void quest_attend_part_kernel(S
   const int bh = blockIdx.x / a.parts, part = blockIdx.x - bh * a.parts;
   attend_item<ROWS, KPT, kHeadWaves, kHeadTiles, kHeadDepth, kMaxParts, true, kStepMaxTopK>(
       a, bh, part, smem_raw, &s_last, s_pages);
-}
-
-// The Quest step's attention (after the score launch, and over given rows for
-// quest_hisparse, so that both compute the same partials in the same order):
-// one 4-wave block per (request, KV head, part), blockIdx = (request, KV head)
-// * parts + part.
-template <bool ROWS, int KPT>
-__global__ __launch_bounds__(64 * kW4Waves, 4) void quest_attend_w4_kernel(StepArgs a) {
-  extern __shared__ __align__(16) unsigned char smem_raw[];
-  __shared__ uint32_t s_last;
-  __shared__ int32_t s_pages[kMaxSelFused];
-  const int bh = blockIdx.x / a.parts, part = blockIdx.x - bh * a.parts;
-  attend_item<ROWS, KPT, kW4Waves, 1, 1, kW4Parts, false, kW4RowCap>(a, bh, part, smem_raw, &s_last, s_pages);
 }
 
 // ------------------------------------------------------- per-page-unit attention
@@ -671,7 +654,7 @@ __global__ __launch_bounds__(64 * W, 8 / W) void quest_attend_unit_kernel(StepAr
   bool poison = false;
   if constexpr (ROWS) poison = __syncthreads_or(bad ? 1 : 0) != 0;  // a failed swap-in: NaN output
   else lds_barrier();  // the selection's LDS is free before the combine reuses it
-  finish_block<W, kW4Parts, false>(a, bh, part, M, L, o, poison, sm.comb.m, sm.comb.l, sm.comb.o, &s_last);
+  finish_block<W, kUnitParts, false>(a, bh, part, M, L, o, poison, sm.comb.m, sm.comb.l, sm.comb.o, &s_last);
 }
 
 }  // namespace
@@ -761,7 +744,7 @@ static bool fused_shape(int q_dtype, int kv_dtype, int new_dtype, int num_q_head
     return false;
   return q_dtype == QQ_DTYPE_BF16 && kv_dtype == QQ_DTYPE_BF16 && (new_dtype < 0 || new_dtype == QQ_DTYPE_BF16) &&
          num_q_heads / kv_heads <= kStepMaxG && top_k / page_size - 1 <= kMaxSelFused && top_k <= kStepMaxTopK &&
-         max_pages <= 24 * 64 * kW4Waves;
+         max_pages <= 24 * 64 * kUnitMinWaves;
 }
 
 // Waves per block of the unit attention: 8 (one block per CU) when the batch has
@@ -770,7 +753,7 @@ static int unit_waves(int bs, int top_k) {
   return (int64_t)bs * kStepKV * (top_k / 64) >= 8LL * device_cu_count() ? 8 : 4;
 }
 // Blocks per (request, KV head): one unit per wave where the parts allow it.
-static int step_parts(int top_k, int waves) { return max(1, min(kW4Parts, ceil_div(top_k / 64, waves))); }
+static int step_parts(int top_k, int waves) { return max(1, min(kUnitParts, ceil_div(top_k / 64, waves))); }
 
 extern "C" int qq_quest_fused_step(int q_dtype, int kv_dtype, int new_dtype, int num_q_heads, int kv_heads,
                                    int head_dim, int page_size, int top_k, int max_pages) {
