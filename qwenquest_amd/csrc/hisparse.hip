@@ -320,29 +320,73 @@ __global__ __launch_bounds__(kPlanThreads) void swap_plan_kernel(SwapArgs a) {
   }
 }
 
-// Host -> device rows of the planned misses: grid (top_k / 4, bs), 64 threads per row.
+// Host -> device rows of the planned misses, read over PCIe by the kernel (zero-copy):
+// grid (top_k / 64, bs), one block per 64 consecutive misses of a request.  Wave w
+// copies misses w, w + 4, ..., w + 60 of its block: with 1 KiB rows (bf16, KV*D = 512)
+// all 32 16-byte loads of its 16 K and V rows are in flight at once, and the block's 4
+// waves read neighbouring host rows together (misses of one page are consecutive host
+// rows).  Other row sizes copy one row at a time per wave.  Rows outside their buffers
+// are skipped.
+constexpr int kCopyRowsPerBlock = 64;
+constexpr int kCopyRowsPerWave = kCopyRowsPerBlock / 4;
+
 __global__ __launch_bounds__(256) void swap_copy_kernel(const int64_t* copy_dst, const int64_t* copy_src,
                                                        const int32_t* copy_count, int top_k,
                                                        char* dev_k, char* dev_v, const char* host_k,
                                                        const char* host_v, int64_t row_bytes,
                                                        int64_t dev_rows, int64_t host_rows) {
   const int b = blockIdx.y;
-  const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (r >= copy_count[b]) return;
-  const int64_t dst = copy_dst[(int64_t)b * top_k + r];
-  const int64_t src = copy_src[(int64_t)b * top_k + r];
-  if (dst < 0 || dst >= dev_rows || src < 0 || src >= host_rows) return;
-  const int lane = threadIdx.x & 63;
+  const int r0 = blockIdx.x * kCopyRowsPerBlock;
+  const int count = min(copy_count[b], top_k);
+  if (r0 >= count) return;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t* dsts = copy_dst + (int64_t)b * top_k;
+  const int64_t* srcs = copy_src + (int64_t)b * top_k;
+  if (row_bytes == 64 * 16) {  // one 16-byte piece per lane and row
+    int64_t dst[kCopyRowsPerWave], src[kCopyRowsPerWave];
+    bool ok[kCopyRowsPerWave];
+    uint4 x[kCopyRowsPerWave], y[kCopyRowsPerWave];
+    // every row's indices first, then every row's data: no data load waits for more
+    // than the index loads
+#pragma unroll
+    for (int i = 0; i < kCopyRowsPerWave; ++i) {
+      const int r = r0 + wave + 4 * i;
+      dst[i] = r < count ? dsts[r] : -1;
+      src[i] = r < count ? srcs[r] : -1;
+    }
+#pragma unroll
+    for (int i = 0; i < kCopyRowsPerWave; ++i) {
+      ok[i] = dst[i] >= 0 && dst[i] < dev_rows && src[i] >= 0 && src[i] < host_rows;  // wave-uniform
+      if (ok[i]) {
+        x[i] = reinterpret_cast<const uint4*>(host_k + src[i] * row_bytes)[lane];
+        y[i] = reinterpret_cast<const uint4*>(host_v + src[i] * row_bytes)[lane];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kCopyRowsPerWave; ++i) {
+      if (ok[i]) {
+        reinterpret_cast<uint4*>(dev_k + dst[i] * row_bytes)[lane] = x[i];
+        reinterpret_cast<uint4*>(dev_v + dst[i] * row_bytes)[lane] = y[i];
+      }
+    }
+    return;
+  }
   const int64_t units = row_bytes / 16;
-  const uint4* hk = reinterpret_cast<const uint4*>(host_k + src * row_bytes);
-  const uint4* hv = reinterpret_cast<const uint4*>(host_v + src * row_bytes);
-  uint4* dk = reinterpret_cast<uint4*>(dev_k + dst * row_bytes);
-  uint4* dv = reinterpret_cast<uint4*>(dev_v + dst * row_bytes);
-  for (int64_t u = lane; u < units; u += 64) {
-    const uint4 x = hk[u];
-    const uint4 y = hv[u];
-    dk[u] = x;
-    dv[u] = y;
+  for (int i = 0; i < kCopyRowsPerWave; ++i) {
+    const int r = r0 + wave + 4 * i;
+    if (r >= count) break;
+    const int64_t d = dsts[r], src = srcs[r];
+    if (d < 0 || d >= dev_rows || src < 0 || src >= host_rows) continue;
+    const uint4* hk = reinterpret_cast<const uint4*>(host_k + src * row_bytes);
+    const uint4* hv = reinterpret_cast<const uint4*>(host_v + src * row_bytes);
+    uint4* dk = reinterpret_cast<uint4*>(dev_k + d * row_bytes);
+    uint4* dv = reinterpret_cast<uint4*>(dev_v + d * row_bytes);
+    for (int64_t u = lane; u < units; u += 64) {
+      const uint4 xv = hk[u];
+      const uint4 yv = hv[u];
+      dk[u] = xv;
+      dv[u] = yv;
+    }
   }
 }
 
@@ -630,7 +674,7 @@ extern "C" int qq_hisparse_swap_in(const int32_t* positions, int64_t positions_s
   a.table_size = T;
   hipStream_t s = static_cast<hipStream_t>(stream);
   swap_plan_kernel<<<bs, kPlanThreads, smem, s>>>(a);
-  swap_copy_kernel<<<dim3((top_k + 3) / 4, bs), 256, 0, s>>>(
+  swap_copy_kernel<<<dim3((top_k + kCopyRowsPerBlock - 1) / kCopyRowsPerBlock, bs), 256, 0, s>>>(
       copy_dst, copy_src, copy_count, top_k, static_cast<char*>(device_k_layer),
       static_cast<char*>(device_v_layer), static_cast<const char*>(host_k_layer),
       static_cast<const char*>(host_v_layer), row_bytes,
