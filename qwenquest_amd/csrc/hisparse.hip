@@ -22,8 +22,8 @@
 //   included) reads its position's slot from the table.  Both error conditions
 //   of the reference (too few victims, coordinator.py:278-279; a position
 //   without host backup, :285-286) are detected before any state is written
-//   and reported through a device error word.  A second grid-wide kernel then
-//   copies the missed rows host -> device.
+//   and reported through a device error word.  A second kernel copies the missed
+//   rows host -> device.
 #include "qq_quest_dev.h"
 
 namespace qq {
@@ -31,7 +31,11 @@ namespace {
 
 constexpr int kPlanThreads = 1024;
 constexpr int kPlanWaves = kPlanThreads / 64;
-constexpr int kMaxPerThread = 8;  // buf <= 8192, top_k <= 8192 entries per thread loop bound
+constexpr int kMaxPerThread = 8;  // buf <= 8192, top_k <= 8192: entries per thread, general form
+// the plan kernel's small form (top_k <= 2048, buf <= 4096): 2 entries and 4 LRU slots per
+// thread, so that its per-thread state and the miss copy fit without spills
+constexpr int kSmallEntries = 2;
+constexpr int kSmallSlots = 4;
 constexpr int kEmpty = -1;
 constexpr int kErrVictims = 1;
 constexpr int kErrHostRow = 2;
@@ -56,7 +60,13 @@ struct SwapArgs {
   unsigned long long* stats;  // hits, misses, fast_path_calls
   int32_t* err;
   int32_t* err_mirror;  // host-mapped words set to 1 per error kind (may be null)
-  int table_size;  // power of two >= 2 * top_k
+  int table_size;  // power of two >= 2 * top_k (4 * top_k when the LDS holds it)
+  // the misses' copy (swap_copy_kernel): host tier rows -> hot buffer rows of this layer
+  char* dev_k;
+  char* dev_v;
+  const char* host_k;
+  const char* host_v;
+  int64_t row_bytes, dev_rows, host_rows;
 };
 
 __device__ inline uint32_t slot_hash(int p, int mask) {
@@ -96,6 +106,79 @@ __device__ inline int block_scan(int v, int* s_wave, int* total) {
   return wave_base + x - v;
 }
 
+__device__ __forceinline__ int64_t wave_first(int64_t v) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)((uint64_t)v >> 32));
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
+// One round of the miss copy for 1 KiB rows (bf16, KV*D = 512): wave w copies misses
+// base + w + NW*i, i < RPW, one 16-byte piece per lane and row.  Every row's indices are
+// loaded first, then every row's K and V data, so that no data load waits for more than
+// the index loads and all 2 * RPW loads of the wave are in flight at once.  The data
+// loads go through a buffer resource per row whose size is 0 for a row that is not
+// copied (past the count or out of its buffer): such a load reads zeros without touching
+// memory, so every load is unconditional and the row data stays in registers.
+template <int NW, int RPW>
+__device__ __forceinline__ void copy_miss_round_1k(const SwapArgs& a, const int64_t* dsts, const int64_t* srcs,
+                                                   int count, int base, int wave, int lane) {
+  int64_t dst[RPW], src[RPW];
+#pragma unroll
+  for (int i = 0; i < RPW; ++i) {
+    const int r = base + wave + NW * i;
+    dst[i] = r < count ? dsts[r] : -1;
+    src[i] = r < count ? srcs[r] : -1;
+  }
+  bool ok[RPW];
+  u32x4_t x[RPW], y[RPW];
+#pragma unroll
+  for (int i = 0; i < RPW; ++i) {
+    dst[i] = wave_first(dst[i]);  // one row per wave: every lane loaded the same index
+    src[i] = wave_first(src[i]);
+    ok[i] = dst[i] >= 0 && dst[i] < a.dev_rows && src[i] >= 0 && src[i] < a.host_rows;
+    const int64_t row = ok[i] ? src[i] : 0;
+    const int bytes = ok[i] ? 1024 : 0;
+    x[i] = __builtin_amdgcn_raw_buffer_load_b128(
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(a.host_k + row * 1024), (short)0, bytes, 0x00020000),
+        lane * 16, 0, 0);
+    y[i] = __builtin_amdgcn_raw_buffer_load_b128(
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(a.host_v + row * 1024), (short)0, bytes, 0x00020000),
+        lane * 16, 0, 0);
+  }
+#pragma unroll
+  for (int i = 0; i < RPW; ++i) {
+    if (ok[i]) {
+      reinterpret_cast<u32x4_t*>(a.dev_k + dst[i] * 1024)[lane] = x[i];
+      reinterpret_cast<u32x4_t*>(a.dev_v + dst[i] * 1024)[lane] = y[i];
+    }
+  }
+}
+
+// Exclusive block scan of one uint64 per thread (fields added without carries by the
+// caller's choice of widths); returns the prefix, *total = sum.
+__device__ inline uint64_t block_scan_u64(uint64_t v, uint64_t* s_wave, uint64_t* total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  uint64_t x = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t lo = (uint32_t)__shfl_up((int)(uint32_t)x, off, 64);
+    const uint32_t hi = (uint32_t)__shfl_up((int)(uint32_t)(x >> 32), off, 64);
+    if (lane >= off) x += ((uint64_t)hi << 32) | lo;
+  }
+  if (lane == 63) s_wave[wave] = x;
+  __syncthreads();
+  uint64_t wave_base = 0, sum = 0;
+  for (int w = 0; w < kPlanWaves; ++w) {
+    const uint64_t t = s_wave[w];
+    if (w < wave) wave_base += t;
+    sum += t;
+  }
+  __syncthreads();
+  *total = sum;
+  return wave_base + x - v;
+}
+
+template <int KT, int KE>
 __global__ __launch_bounds__(kPlanThreads) void swap_plan_kernel(SwapArgs a) {
   extern __shared__ __align__(16) int smem[];
   const int b = blockIdx.x, tid = threadIdx.x;
@@ -126,6 +209,8 @@ __global__ __launch_bounds__(kPlanThreads) void swap_plan_kernel(SwapArgs a) {
   int* s_tok = s_vic + a.top_k;      // [buf] position cached by each slot (-1 none)
   int* s_wave = s_tok + buf;         // [kPlanWaves]
   int* s_flag = s_wave + kPlanWaves; // [1] host-row error
+  // [kPlanWaves] 64-bit scan totals, 8-byte aligned after the flag
+  uint64_t* s_wave64 = reinterpret_cast<uint64_t*>(s_flag + 1 + ((buf + a.top_k + 1) & 1));
   int64_t* tok = a.tokens + req * (int64_t)buf;
   int64_t* lru = a.lru + req * (int64_t)buf;
   const int E = (buf + kPlanThreads - 1) / kPlanThreads;  // LRU entries per thread (a contiguous run)
@@ -133,19 +218,22 @@ __global__ __launch_bounds__(kPlanThreads) void swap_plan_kernel(SwapArgs a) {
   // Every global load that does not depend on another goes out first: the entries'
   // positions (i = tid + k*1024), the LRU order (j = tid*E + e) and every slot's token
   // (t = tid + e*1024); the entries' host rows follow as soon as their positions are in.
-  int my_p[kMaxPerThread], my_slot[kMaxPerThread];
-  int64_t my_tok[kMaxPerThread], my_host[kMaxPerThread];
+  int my_p[KT], my_slot[KE];
+  int64_t my_tok[KE], my_host[KT];
 #pragma unroll
-  for (int k = 0; k < kMaxPerThread; ++k) {
+  for (int k = 0; k < KT; ++k) {
     const int i = tid + k * kPlanThreads;
     my_p[k] = i < n ? pos[i] : -1;
+  }
+#pragma unroll
+  for (int k = 0; k < KE; ++k) {
     const int j = tid * E + k;
     my_slot[k] = (k < E && j < buf) ? (int)lru[j] : -1;
     const int t = tid + k * kPlanThreads;
     my_tok[k] = t < buf ? tok[t] : -1;
   }
 #pragma unroll
-  for (int k = 0; k < kMaxPerThread; ++k) {
+  for (int k = 0; k < KT; ++k) {
     const int64_t p = my_p[k];
     my_host[k] = (p >= 0 && p < a.r2h_stride) ? a.r2h[req * a.r2h_stride + p] : -1;
   }
@@ -155,18 +243,18 @@ __global__ __launch_bounds__(kPlanThreads) void swap_plan_kernel(SwapArgs a) {
   }
   if (tid == 0) *s_flag = 0;
 #pragma unroll
-  for (int k = 0; k < kMaxPerThread; ++k) {
+  for (int k = 0; k < KE; ++k) {
     const int t = tid + k * kPlanThreads;
     if (t < buf) s_tok[t] = (my_tok[k] >= 0 && my_tok[k] < 0x7FFFFFFF) ? (int)my_tok[k] : -1;
   }
   lds_barrier();  // LDS-only: the host-row loads stay in flight
 
   // dedup: insert every non-newest entry, keeping the smallest entry index (first occurrence)
-  int my_h[kMaxPerThread];
-  bool my_new[kMaxPerThread];
+  int my_h[KT];
+  bool my_new[KT];
   const int64_t newest_pos = s - 1;
 #pragma unroll
-  for (int k = 0; k < kMaxPerThread; ++k) {
+  for (int k = 0; k < KT; ++k) {
     const int i = tid + k * kPlanThreads;
     my_h[k] = -1;
     my_new[k] = false;
@@ -188,9 +276,9 @@ __global__ __launch_bounds__(kPlanThreads) void swap_plan_kernel(SwapArgs a) {
     }
   }
   lds_barrier();
-  bool my_first[kMaxPerThread];
+  bool my_first[KT];
 #pragma unroll
-  for (int k = 0; k < kMaxPerThread; ++k) {
+  for (int k = 0; k < KT; ++k) {
     const int i = tid + k * kPlanThreads;
     my_first[k] = i < n && !my_new[k] && my_h[k] >= 0 && s_val[my_h[k]] == i;
   }
@@ -199,9 +287,9 @@ __global__ __launch_bounds__(kPlanThreads) void swap_plan_kernel(SwapArgs a) {
   lds_barrier();
 
   // hits: the LRU run j = tid*E + e looks its slot's token up in the table
-  bool my_hit[kMaxPerThread];
+  bool my_hit[KE];
 #pragma unroll
-  for (int e = 0; e < kMaxPerThread; ++e) {
+  for (int e = 0; e < KE; ++e) {
     my_hit[e] = false;
     const int slot = my_slot[e];
     const int t = (slot >= 0 && slot < buf) ? s_tok[slot] : -1;
@@ -216,31 +304,44 @@ __global__ __launch_bounds__(kPlanThreads) void swap_plan_kernel(SwapArgs a) {
   lds_barrier();
 
   // misses: first occurrences without a hit, ranked in entry order (entry i = tid + k*1024
-  // is not contiguous per thread, so rank by a scan per k-round; rounds past n hold none)
+  // is not contiguous per thread, so the ranks come from a scan per k-round); evictable
+  // (non-hit) LRU entries ranked in LRU order; unique entries counted.  The first two
+  // rounds, the evictable count and the unique count go through one scan of four 16-bit
+  // counters (each total <= 8192, so no field carries into the next); rounds past the
+  // second (top_k > 2048) take a scan each.
   const int rounds = (n + kPlanThreads - 1) / kPlanThreads;
   int uniq_local = 0;
-  int miss_rank[kMaxPerThread];
-  int num_miss = 0;
+  bool miss_k[KT];
 #pragma unroll
-  for (int k = 0; k < kMaxPerThread; ++k) {
-    miss_rank[k] = -1;
-    if (k >= rounds) continue;  // block-uniform
-    const bool miss = my_first[k] && s_val[my_h[k] >= 0 ? my_h[k] : 0] < 0;
-    uniq_local += my_first[k] ? 1 : 0;
-    int tot;
-    const int r = block_scan(miss ? 1 : 0, s_wave, &tot);
-    miss_rank[k] = miss ? num_miss + r : -1;
-    num_miss += tot;
+  for (int k = 0; k < KT; ++k) {
+    miss_k[k] = k < rounds && my_first[k] && s_val[my_h[k] >= 0 ? my_h[k] : 0] < 0;
+    uniq_local += (k < rounds && my_first[k]) ? 1 : 0;
   }
-  // evictable (non-hit) and hit ranks in LRU order
   int ev_local = 0;
 #pragma unroll
-  for (int e = 0; e < kMaxPerThread; ++e)
+  for (int e = 0; e < KE; ++e)
     if (e < E && tid * E + e < buf && !my_hit[e]) ++ev_local;
-  int n_ev;
-  const int ev_base = block_scan(ev_local, s_wave, &n_ev);
-  int uniq_total;
-  (void)block_scan(uniq_local, s_wave, &uniq_total);
+  uint64_t packed_total;
+  const uint64_t packed = block_scan_u64((uint64_t)(miss_k[0] ? 1 : 0) | ((uint64_t)(miss_k[1] ? 1 : 0) << 16) |
+                                             ((uint64_t)ev_local << 32) | ((uint64_t)uniq_local << 48),
+                                         s_wave64, &packed_total);
+  int miss_rank[KT];
+  miss_rank[0] = miss_k[0] ? (int)(packed & 0xFFFFu) : -1;
+  int num_miss = (int)(packed_total & 0xFFFFu);
+  miss_rank[1] = miss_k[1] ? num_miss + (int)((packed >> 16) & 0xFFFFu) : -1;
+  num_miss += (int)((packed_total >> 16) & 0xFFFFu);
+#pragma unroll
+  for (int k = 2; k < KT; ++k) {
+    miss_rank[k] = -1;
+    if (k >= rounds) continue;  // block-uniform
+    int tot;
+    const int r = block_scan(miss_k[k] ? 1 : 0, s_wave, &tot);
+    miss_rank[k] = miss_k[k] ? num_miss + r : -1;
+    num_miss += tot;
+  }
+  const int ev_base = (int)((packed >> 32) & 0xFFFFu);
+  const int n_ev = (int)((packed_total >> 32) & 0xFFFFu);
+  const int uniq_total = (int)((packed_total >> 48) & 0xFFFFu);
   if (num_miss > n_ev) {  // coordinator.py:278-279
     if (tid == 0) {
       atomicOr(a.err, kErrVictims);
@@ -253,7 +354,7 @@ __global__ __launch_bounds__(kPlanThreads) void swap_plan_kernel(SwapArgs a) {
   {
     int e_rank = ev_base;
 #pragma unroll
-    for (int e = 0; e < kMaxPerThread; ++e) {
+    for (int e = 0; e < KE; ++e) {
       if (e < E && tid * E + e < buf && !my_hit[e]) {
         if (e_rank < num_miss) s_vic[e_rank] = my_slot[e];
         ++e_rank;
@@ -265,7 +366,7 @@ __global__ __launch_bounds__(kPlanThreads) void swap_plan_kernel(SwapArgs a) {
   int64_t* cdst = a.copy_dst + (int64_t)b * a.top_k;
   int64_t* csrc = a.copy_src + (int64_t)b * a.top_k;
 #pragma unroll
-  for (int k = 0; k < kMaxPerThread; ++k) {
+  for (int k = 0; k < KT; ++k) {
     if (miss_rank[k] >= 0) {
       const int slot = s_vic[miss_rank[k]];
       const int64_t host = my_host[k];
@@ -287,12 +388,12 @@ __global__ __launch_bounds__(kPlanThreads) void swap_plan_kernel(SwapArgs a) {
   }
   // commit: tokens of the victims, new LRU order (coordinator.py:291, 295)
 #pragma unroll
-  for (int k = 0; k < kMaxPerThread; ++k)
+  for (int k = 0; k < KT; ++k)
     if (miss_rank[k] >= 0) tok[s_vic[miss_rank[k]]] = my_p[k];
   {
     int e_rank = ev_base, h_rank = min(tid * E, buf) - ev_base;  // hits before this thread's run
 #pragma unroll
-    for (int e = 0; e < kMaxPerThread; ++e) {
+    for (int e = 0; e < KE; ++e) {
       if (e < E && tid * E + e < buf) {
         int dst;
         if (!my_hit[e]) {
@@ -308,7 +409,7 @@ __global__ __launch_bounds__(kPlanThreads) void swap_plan_kernel(SwapArgs a) {
   }
   // rows of every entry, duplicates included (coordinator.py:298-300)
 #pragma unroll
-  for (int k = 0; k < kMaxPerThread; ++k) {
+  for (int k = 0; k < KT; ++k) {
     const int i = tid + k * kPlanThreads;
     if (i < n) rows[i] = my_new[k] ? base_row + buf : base_row + s_val[my_h[k]];
   }
@@ -321,66 +422,35 @@ __global__ __launch_bounds__(kPlanThreads) void swap_plan_kernel(SwapArgs a) {
 }
 
 // Host -> device rows of the planned misses, read over PCIe by the kernel (zero-copy):
-// grid (top_k / 64, bs), one block per 64 consecutive misses of a request.  Wave w
-// copies misses w, w + 4, ..., w + 60 of its block: with 1 KiB rows (bf16, KV*D = 512)
-// all 32 16-byte loads of its 16 K and V rows are in flight at once, and the block's 4
-// waves read neighbouring host rows together (misses of one page are consecutive host
-// rows).  Other row sizes copy one row at a time per wave.  Rows outside their buffers
-// are skipped.
+// grid (top_k / 64, bs), one block per 64 consecutive misses of a request.  Wave w copies
+// misses w, w + 4, ..., w + 60 of its block: with 1 KiB rows all 32 16-byte loads of its
+// 16 K and V rows are in flight at once, and the block's 4 waves read neighbouring host
+// rows together (the misses of one page are consecutive host rows).  Other row sizes copy
+// one row at a time per wave.  Rows outside their buffers are skipped.
 constexpr int kCopyRowsPerBlock = 64;
-constexpr int kCopyRowsPerWave = kCopyRowsPerBlock / 4;
+constexpr int kCopyWaves = 4;
 
-__global__ __launch_bounds__(256) void swap_copy_kernel(const int64_t* copy_dst, const int64_t* copy_src,
-                                                       const int32_t* copy_count, int top_k,
-                                                       char* dev_k, char* dev_v, const char* host_k,
-                                                       const char* host_v, int64_t row_bytes,
-                                                       int64_t dev_rows, int64_t host_rows) {
+__global__ __launch_bounds__(kCopyWaves * 64) void swap_copy_kernel(SwapArgs a) {
   const int b = blockIdx.y;
   const int r0 = blockIdx.x * kCopyRowsPerBlock;
-  const int count = min(copy_count[b], top_k);
+  const int count = min(a.copy_count[b], a.top_k);
   if (r0 >= count) return;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int64_t* dsts = copy_dst + (int64_t)b * top_k;
-  const int64_t* srcs = copy_src + (int64_t)b * top_k;
-  if (row_bytes == 64 * 16) {  // one 16-byte piece per lane and row
-    int64_t dst[kCopyRowsPerWave], src[kCopyRowsPerWave];
-    bool ok[kCopyRowsPerWave];
-    uint4 x[kCopyRowsPerWave], y[kCopyRowsPerWave];
-    // every row's indices first, then every row's data: no data load waits for more
-    // than the index loads
-#pragma unroll
-    for (int i = 0; i < kCopyRowsPerWave; ++i) {
-      const int r = r0 + wave + 4 * i;
-      dst[i] = r < count ? dsts[r] : -1;
-      src[i] = r < count ? srcs[r] : -1;
-    }
-#pragma unroll
-    for (int i = 0; i < kCopyRowsPerWave; ++i) {
-      ok[i] = dst[i] >= 0 && dst[i] < dev_rows && src[i] >= 0 && src[i] < host_rows;  // wave-uniform
-      if (ok[i]) {
-        x[i] = reinterpret_cast<const uint4*>(host_k + src[i] * row_bytes)[lane];
-        y[i] = reinterpret_cast<const uint4*>(host_v + src[i] * row_bytes)[lane];
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < kCopyRowsPerWave; ++i) {
-      if (ok[i]) {
-        reinterpret_cast<uint4*>(dev_k + dst[i] * row_bytes)[lane] = x[i];
-        reinterpret_cast<uint4*>(dev_v + dst[i] * row_bytes)[lane] = y[i];
-      }
-    }
+  const int64_t* dsts = a.copy_dst + (int64_t)b * a.top_k;
+  const int64_t* srcs = a.copy_src + (int64_t)b * a.top_k;
+  if (a.row_bytes == 1024) {
+    copy_miss_round_1k<kCopyWaves, kCopyRowsPerBlock / kCopyWaves>(a, dsts, srcs, count, r0, wave, lane);
     return;
   }
-  const int64_t units = row_bytes / 16;
-  for (int i = 0; i < kCopyRowsPerWave; ++i) {
-    const int r = r0 + wave + 4 * i;
-    if (r >= count) break;
+  const int64_t row_bytes = a.row_bytes, units = row_bytes / 16;
+  const int r1 = min(count, r0 + kCopyRowsPerBlock);
+  for (int r = r0 + wave; r < r1; r += kCopyWaves) {
     const int64_t d = dsts[r], src = srcs[r];
-    if (d < 0 || d >= dev_rows || src < 0 || src >= host_rows) continue;
-    const uint4* hk = reinterpret_cast<const uint4*>(host_k + src * row_bytes);
-    const uint4* hv = reinterpret_cast<const uint4*>(host_v + src * row_bytes);
-    uint4* dk = reinterpret_cast<uint4*>(dev_k + d * row_bytes);
-    uint4* dv = reinterpret_cast<uint4*>(dev_v + d * row_bytes);
+    if (d < 0 || d >= a.dev_rows || src < 0 || src >= a.host_rows) continue;
+    const uint4* hk = reinterpret_cast<const uint4*>(a.host_k + src * row_bytes);
+    const uint4* hv = reinterpret_cast<const uint4*>(a.host_v + src * row_bytes);
+    uint4* dk = reinterpret_cast<uint4*>(a.dev_k + d * row_bytes);
+    uint4* dv = reinterpret_cast<uint4*>(a.dev_v + d * row_bytes);
     for (int64_t u = lane; u < units; u += 64) {
       const uint4 xv = hk[u];
       const uint4 yv = hv[u];
@@ -615,9 +685,12 @@ static int plan_lds_opt_in() {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return set_error(QQ_EHIP, "qq_hisparse_swap_in: no device");
   if (!opted[dev]) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&swap_plan_kernel),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, kPlanMaxLds);
-    if (e != hipSuccess) return set_error(QQ_EHIP, "qq_hisparse_swap_in: LDS opt-in failed: %s", hipGetErrorString(e));
+    const void* kernels[2] = {reinterpret_cast<const void*>(&swap_plan_kernel<kSmallEntries, kSmallSlots>),
+                              reinterpret_cast<const void*>(&swap_plan_kernel<kMaxPerThread, kMaxPerThread>)};
+    for (const void* k : kernels) {
+      const hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, kPlanMaxLds);
+      if (e != hipSuccess) return set_error(QQ_EHIP, "qq_hisparse_swap_in: LDS opt-in failed: %s", hipGetErrorString(e));
+    }
     opted[dev] = true;
   }
   return QQ_OK;
@@ -644,9 +717,15 @@ extern "C" int qq_hisparse_swap_in(const int32_t* positions, int64_t positions_s
              what, (long long)row_bytes);
   QQ_REQUIRE(positions_stride >= top_k, "%s: positions stride < top_k", what);
   if (bs == 0) return QQ_OK;
+  // the dedup table: a power of two >= 4 * top_k when the LDS holds it (short probe
+  // chains for the hit lookups), else >= 2 * top_k
+  auto plan_smem = [&](int t) {
+    return (size_t)(2 * t + top_k + device_buffer_size + kPlanWaves + 2) * sizeof(int) + kPlanWaves * sizeof(uint64_t);
+  };
   int T = 1;
-  while (T < 2 * top_k) T <<= 1;
-  const size_t smem = (size_t)(2 * T + top_k + device_buffer_size + kPlanWaves + 1) * sizeof(int);
+  while (T < 4 * top_k) T <<= 1;
+  if (plan_smem(T) > (size_t)kPlanMaxLds) T >>= 1;
+  const size_t smem = plan_smem(T);
   QQ_REQUIRE(smem <= kPlanMaxLds, "%s: top_k %d with a %d-slot buffer needs %zu bytes of LDS (at most %d)", what,
              top_k, device_buffer_size, smem, kPlanMaxLds);
   if (smem > 64 * 1024 && plan_lds_opt_in() != QQ_OK) return QQ_EHIP;
@@ -672,13 +751,19 @@ extern "C" int qq_hisparse_swap_in(const int32_t* positions, int64_t positions_s
   a.err = error_flags;
   a.err_mirror = error_mirror;
   a.table_size = T;
+  a.dev_k = static_cast<char*>(device_k_layer);
+  a.dev_v = static_cast<char*>(device_v_layer);
+  a.host_k = static_cast<const char*>(host_k_layer);
+  a.host_v = static_cast<const char*>(host_v_layer);
+  a.row_bytes = row_bytes;
+  a.dev_rows = (int64_t)max_reqs * (device_buffer_size + 1);
+  a.host_rows = host_rows;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  swap_plan_kernel<<<bs, kPlanThreads, smem, s>>>(a);
-  swap_copy_kernel<<<dim3((top_k + kCopyRowsPerBlock - 1) / kCopyRowsPerBlock, bs), 256, 0, s>>>(
-      copy_dst, copy_src, copy_count, top_k, static_cast<char*>(device_k_layer),
-      static_cast<char*>(device_v_layer), static_cast<const char*>(host_k_layer),
-      static_cast<const char*>(host_v_layer), row_bytes,
-      (int64_t)max_reqs * (device_buffer_size + 1), host_rows);
+  if (top_k <= kSmallEntries * kPlanThreads && device_buffer_size <= kSmallSlots * kPlanThreads)
+    swap_plan_kernel<kSmallEntries, kSmallSlots><<<bs, kPlanThreads, smem, s>>>(a);
+  else
+    swap_plan_kernel<kMaxPerThread, kMaxPerThread><<<bs, kPlanThreads, smem, s>>>(a);
+  swap_copy_kernel<<<dim3((top_k + kCopyRowsPerBlock - 1) / kCopyRowsPerBlock, bs), kCopyWaves * 64, 0, s>>>(a);
   return check_launch(what);
 }
 
