@@ -92,12 +92,15 @@ def test_swap_in_is_exact_under_random_selections(prefill_len, buf, top_k):
     assert stats.misses > 0 and (stats.hits, stats.misses) == (st.hits, st.misses)
 
 
-@pytest.mark.parametrize(("prefill_len", "buf", "top_k"), [(1200, 1025, 512), (2000, 1500, 1024), (5000, 4097, 2048)])
+@pytest.mark.parametrize(("prefill_len", "buf", "top_k"),
+                         [(1200, 1025, 512), (2000, 1500, 1024), (5000, 4096, 2048), (5000, 4097, 2048),
+                          (7000, 6000, 3000)])
 def test_swap_in_large_buffers_match_oracle(prefill_len, buf, top_k):
     """Hot buffers that are not a multiple of the plan block's 1024 threads and exceed it
-    (each thread holds a run of ceil(buf / 1024) LRU entries, the last runs partial or empty;
-    4097 is the benchmark's 4096 + 1): rows, buffer_tokens, lru_slots and hit/miss counts
-    equal the oracle's at every step, with duplicated and newest-token entries."""
+    (each thread holds a run of ceil(buf / 1024) LRU entries, the last runs partial or empty),
+    on both sides of the plan kernel's small form (top_k <= 2048 and buf <= 4096) and with
+    more than two 1024-entry rounds (top_k 3000): rows, buffer_tokens, lru_slots and hit/miss
+    counts equal the oracle's at every step, with duplicated and newest-token entries."""
     steps = 24
     total = prefill_len + steps
     k, v = truth(total, seed=3)
