@@ -118,9 +118,10 @@ def test_batch8_32k_per_page_offsets():
 def test_ragged_48_layer_sweep_sampled():
     """48 layers, batch 16, contexts uniform in [8192, 131072] (seeded), 64 decode steps with
     one append per request per step, all layers through QuestOnlyBackend.  Sampled
-    (layer, request) pairs follow the oracle from their own K rows: positions bit-exact at
-    sampled steps, attention within attn_tol, and the pair's page bounds / running bounds
-    bit-exact after the last step (pages completed during the sweep included)."""
+    (layer, request) pairs - every request in one layer, 19 pairs - follow the oracle from
+    their own K rows: positions bit-exact at every step, attention within attn_tol at sampled
+    steps, and the pair's page bounds / running bounds bit-exact after the last step (pages
+    completed during the sweep included)."""
     from qwenquest_amd.attention.quest_only import QuestOnlyBackend
     from qwenquest_amd.batch import ForwardBatch, ForwardMode
     from qwenquest_amd.memory import MHATokenToKVPool, ReqToTokenPool
@@ -145,7 +146,10 @@ def test_ragged_48_layer_sweep_sampled():
     for r in range(B):
         be.quest.update_prefill_representations_fused(r, kvp.k_all, rtp.req_to_token[r, : prompts[r]])
         be._skip_first_decode_update[r] = True
-    samples = [(0, int(np.argmax(ctxs))), (23, int(np.argmin(ctxs))), (47, 5)]
+    # every request in one layer (spread over the 48), plus the longest request in layer 0,
+    # the shortest in layer 23 and request 5 in layer 47
+    samples = sorted({(7 * r % L, r) for r in range(B)} | {(0, int(np.argmax(ctxs))), (23, int(np.argmin(ctxs))),
+                                                          (47, 5)})
     oracles = {}
     for layer, r in samples:
         st = oq.QuestState(TOP_K, P)
@@ -173,12 +177,14 @@ def test_ragged_48_layer_sweep_sampled():
         for layer in range(L):
             out = be.forward_decode(q[layer], kn[layer], vn[layer], Layer(layer), batch)
             for (sl, r), st in oracles.items():
-                if sl != layer or step not in check_steps:
+                if sl != layer:
                     continue
                 pos = be._positions[r].cpu().numpy()
                 ref_pos, ref_actual, _ = st.retrieve_topk(q[layer, r : r + 1].float().cpu().numpy(), layer, [0])
                 n = int(ref_actual[0])
                 assert np.array_equal(pos[:n], ref_pos[0, :n]), f"step {step} layer {layer} request {r}"
+                if step not in check_steps:
+                    continue
                 rows = (int(base[r]) + torch.from_numpy(ref_pos[0, :n].astype(np.int64))).to(DEV)
                 ref = oracle_attention(q[layer, r].cpu(), kvp.k_all[layer, rows].cpu(), kvp.v_all[layer, rows].cpu())
                 assert_attn_close(out[r].float().cpu().numpy(), ref, f"step {step} layer {layer}")
@@ -262,6 +268,77 @@ def test_batch4_262k_outliers_quest_and_hisparse(avoid):
         ref_pos, ref_actual, _ = st.retrieve_topk(qs[step].float().cpu().numpy(), 0, reqs)
         for i in range(B):
             n = int(ref_actual[i])
+            assert np.array_equal(poss[step, i, :n].numpy(), ref_pos[i, :n]), f"step {step} request {i}"
+            if step in attn_steps:
+                rows = torch.from_numpy(1 + i * ctx + ref_pos[i, :n].astype(np.int64))
+                ref = oracle_attention(qs[step, i].cpu(), kk[rows], vv[rows])
+                assert_attn_close(outs[step, i].float().numpy(), ref, f"step {step} request {i}")
+
+
+def test_contexts_past_the_fused_selection_400k():
+    """Batch 2 x 400000 tokens (6250 pages, past the 6144 pages the fused step selects from,
+    so QuestOnlyBackend runs the four-launch path), 80 decode steps that complete page 6250:
+    QuestOnlyBackend and QuestHiSparseBackend give bit-identical positions and outputs at
+    every step; positions bit-exact vs the oracle on sampled steps, attention within attn_tol."""
+    from qwenquest_amd import _lib
+    from qwenquest_amd.batch import ForwardBatch, ForwardMode
+
+    B, S, steps = 2, 400000, 80
+    ctx = S + steps + 64
+    assert not _lib.load().qq_quest_fused_step(_lib.DTYPE_BF16, _lib.DTYPE_BF16, _lib.DTYPE_BF16, H, KV, D, P, TOP_K,
+                                               (ctx + P - 1) // P)
+    k = dev_randn((B * ctx + 1, KV, D), 31).to(torch.bfloat16)
+    v = dev_randn((B * ctx + 1, KV, D), 32).to(torch.bfloat16)
+    qs = dev_randn((steps, B, H, D), 33).to(torch.bfloat16)
+    prompt = S - 1
+    kk, vv = k.cpu(), v.cpu()
+    kbits = bf16_bits(kk)
+    st = oq.QuestState(TOP_K, P)
+    st.init_storage(0, 1, B, ctx, KV, D)
+    for r in range(B):
+        st.update_prefill_representations(0, r, kbits, 1 + r * ctx + np.arange(prompt))
+    check_steps = {0, 1, 2, 30, 63, 64, 65, 79}
+    attn_steps = {0, 65, 79}
+    reqs = list(range(B))
+    results = {}
+    for mode in ("quest", "quest_hisparse"):
+        rtp, kvp, be, base = make_quest_backend(B, ctx, 1, hisparse=mode == "quest_hisparse")
+        kvp.k_all[0].copy_(k)
+        kvp.v_all[0].copy_(v)
+        pre = ForwardBatch(ForwardMode.EXTEND, None, None, torch.arange(B), torch.full((B,), prompt), None,
+                           rtp, kvp, be)
+        if mode == "quest":
+            be._update_quest_for_extend(pre)
+        else:
+            be.on_extend_finished(pre)
+        outs, poss = [], []
+        for step in range(steps):
+            seq = torch.full((B,), S + step, device=DEV, dtype=torch.int64)
+            loc = base + seq - 1
+            batch = ForwardBatch(ForwardMode.DECODE, None, None, torch.arange(B, device=DEV), seq,
+                                 loc if mode == "quest" else None, rtp, kvp, be)
+            be.init_forward_metadata(batch)
+            out = be.forward_decode(qs[step], k[loc], v[loc], Layer(0), batch)
+            outs.append(out.cpu())
+            poss.append(be._positions[:B].cpu())
+        results[mode] = (torch.stack(outs), torch.stack(poss))
+        del rtp, kvp, be
+        torch.cuda.empty_cache()
+    assert torch.equal(results["quest"][1], results["quest_hisparse"][1])
+    assert torch.equal(results["quest"][0], results["quest_hisparse"][0])
+    outs, poss = results["quest"]
+    for step in range(steps):
+        seqs = np.full(B, S + step)
+        if step > 0:
+            st.update_decode_representations(0, reqs, kbits, 1 + np.arange(B) * ctx + seqs - 2)
+            st.maybe_finalize_decode_representations(reqs)
+        st.prepare_step(seqs)
+        if step not in check_steps:
+            continue
+        ref_pos, ref_actual, _ = st.retrieve_topk(qs[step].float().cpu().numpy(), 0, reqs)
+        for i in range(B):
+            n = int(ref_actual[i])
+            assert n == TOP_K
             assert np.array_equal(poss[step, i, :n].numpy(), ref_pos[i, :n]), f"step {step} request {i}"
             if step in attn_steps:
                 rows = torch.from_numpy(1 + i * ctx + ref_pos[i, :n].astype(np.int64))
