@@ -201,6 +201,14 @@ def hisparse_measure(B: int, S: int, L: int, warmup: int, steps: int, event_step
     be.on_extend_finished(pre)
     torch.cuda.synchronize()
     setup_s = time.perf_counter() - t_setup
+    prefill = None
+    if B > 1:
+        pf_us = pf0.elapsed_time(pf1) * 1e3
+        pf_bytes = float(sum(int(c) - 1 for c in ctxs[1:])) * L * KV * D * 2  # every prompt key read once
+        prefill = {"kernel": "prefill_bounds_wave_kernel", "requests": B - 1, "layers": L,
+                   "tokens_per_request": int(ctxs[1:].mean()) - 1, "us_per_request": round(pf_us / (B - 1), 1),
+                   "gbs": round(pf_bytes / (pf_us * 1e-6) / 1e9, 1),
+                   "hbm_frac": round(pf_bytes / (pf_us * 1e-6) / (HBM_PEAK_GBS * 1e9), 4)}
 
     coord = be.coord
     layers = [Layer(i, D**-0.5) for i in range(L)]
@@ -344,6 +352,14 @@ def dense_bench(args) -> int:
     batch = ForwardBatch(ForwardMode.DECODE, None, None, torch.arange(B, device=dev), seq_lens, out_loc, rtp, kvp, be)
     torch.cuda.synchronize()
     setup_s = time.perf_counter() - t_setup
+    prefill = None
+    if B > 1:
+        pf_us = pf0.elapsed_time(pf1) * 1e3
+        pf_bytes = float(sum(int(c) - 1 for c in ctxs[1:])) * L * KV * D * 2  # every prompt key read once
+        prefill = {"kernel": "prefill_bounds_wave_kernel", "requests": B - 1, "layers": L,
+                   "tokens_per_request": int(ctxs[1:].mean()) - 1, "us_per_request": round(pf_us / (B - 1), 1),
+                   "gbs": round(pf_bytes / (pf_us * 1e-6) / 1e9, 1),
+                   "hbm_frac": round(pf_bytes / (pf_us * 1e-6) / (HBM_PEAK_GBS * 1e9), 4)}
 
     def step():
         torch.add(base, seq_lens - 1, out=out_loc)
@@ -456,10 +472,15 @@ def main() -> int:
     base = torch.tensor(starts, device=dev, dtype=torch.int64)
     rtp.req_to_token.copy_((base[:, None] + torch.arange(max_ctx, device=dev)[None]).clamp(max=rows).to(torch.int32))
     be = QuestOnlyBackend(rtp, kvp, {"algorithm": "quest", "top_k": TOP_K, "quest_page_size": P})
+    # the prefill bounds build of requests 1 .. B-1 is timed with HIP events (request 0 warms up)
+    pf0, pf1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     for r in range(B):
         # prefill covers positions [0, ctx - 1); the first decode step has seq_len ctx
         be.quest.update_prefill_representations_fused(r, kvp.k_all, rtp.req_to_token[r, : int(ctxs[r]) - 1])
         be._skip_first_decode_update[r] = True
+        if r == 0:
+            pf0.record()
+    pf1.record()
     q_all = torch.randn((L, B, H, D), generator=gen, device=dev).to(torch.bfloat16)
     k_new = torch.randn((L, B, KV, D), generator=gen, device=dev).to(torch.bfloat16)
     v_new = torch.randn((L, B, KV, D), generator=gen, device=dev).to(torch.bfloat16)
@@ -469,6 +490,14 @@ def main() -> int:
     out_loc = torch.empty(B, device=dev, dtype=torch.int64)
     torch.cuda.synchronize()
     setup_s = time.perf_counter() - t_setup
+    prefill = None
+    if B > 1:
+        pf_us = pf0.elapsed_time(pf1) * 1e3
+        pf_bytes = float(sum(int(c) - 1 for c in ctxs[1:])) * L * KV * D * 2  # every prompt key read once
+        prefill = {"kernel": "prefill_bounds_wave_kernel", "requests": B - 1, "layers": L,
+                   "tokens_per_request": int(ctxs[1:].mean()) - 1, "us_per_request": round(pf_us / (B - 1), 1),
+                   "gbs": round(pf_bytes / (pf_us * 1e-6) / 1e9, 1),
+                   "hbm_frac": round(pf_bytes / (pf_us * 1e-6) / (HBM_PEAK_GBS * 1e9), 4)}
 
     batch = ForwardBatch(ForwardMode.DECODE, None, None, rpi, seq_lens, out_loc, rtp, kvp, be)
 
@@ -573,6 +602,7 @@ def main() -> int:
                      "traffic": None if args.ragged else traffic.get(dominant[0]),
                      "traffic_source": traffic_source},
         "cpu_baseline": cpu,
+        "prefill_bounds": prefill,
         "setup_s": round(setup_s, 1),
     }
     if args.hisparse_steps > 0 and not args.ragged:

@@ -71,6 +71,8 @@ __device__ inline int64_t load_index(const void* p, int is64, int64_t i) {
 // rows with independent loads (one row = KV*D contiguous elements, so each
 // row step of the block is one coalesced KV*D-element read).
 constexpr int kRowChunk = 256;
+constexpr int kWaveFoldBatch = 16;  // rows in flight per wave of prefill_bounds_wave_kernel
+constexpr int kWavePages = 1;      // pages per wave of prefill_bounds_wave_kernel
 
 __global__ __launch_bounds__(kThreads) void prefill_bounds_kernel(PrefillArgs a) {
   const int64_t page = blockIdx.x;
@@ -237,6 +239,167 @@ __global__ __launch_bounds__(kThreads) void prefill_bounds_wide_kernel(PrefillAr
     for (int e = 0; e < 8; ++e) {
       a.rmin[rc + e] = mn[e];
       a.rmax[rc + e] = mx[e];
+    }
+  }
+}
+
+// Two bf16 values (the halves of w) as 16-bit keys whose unsigned order is the values'
+// order: x | 0x8000 for a clear sign bit, ~x for a set one.  Away from NaN and from
+// zeros (-0 and +0 are equal values with different keys), equal keys are equal bit
+// patterns, so the unsigned min / max of keys is torch.minimum / maximum of the values.
+typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
+__device__ inline uint32_t bf16x2_key(uint32_t w) { return w ^ ((((w >> 15) & 0x00010001u) * 0x7FFFu) | 0x80008000u); }
+__device__ inline uint32_t bf16x2_unkey(uint32_t k) {
+  return k ^ ((((~k >> 15) & 0x00010001u) * 0x7FFFu) | 0x80008000u);
+}
+__device__ inline uint32_t u16x2_min(uint32_t a, uint32_t b) {
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_min(__builtin_bit_cast(u16x2_t, a), __builtin_bit_cast(u16x2_t, b)));
+}
+__device__ inline uint32_t u16x2_max(uint32_t a, uint32_t b) {
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(u16x2_t, a), __builtin_bit_cast(u16x2_t, b)));
+}
+// max over the halves of (|x| - 1) mod 2^16: >= 0x7F80 exactly when a half is a NaN or a zero
+__device__ inline uint32_t bf16x2_special(uint32_t w) {
+  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2_t, w & 0x7FFF7FFFu) - (u16x2_t){1, 1});
+}
+
+// The wide fold for C = 512 (KV*D = 4 x 128, bf16): one wave per PPW consecutive pages
+// of one layer, 4 waves per block, no LDS and no barrier.  Lane l holds channels 8l ..
+// 8l + 7 of every row (one 1 KiB row per load instruction); a page's row indices come in
+// with one load (lane r: row r of a 64-row chunk; the first chunk of every page of the
+// wave is loaded up front) and reach the row loads through readlane, and the rows fold
+// in order in batches of B loads in flight, so ties and NaNs resolve as in a sequential
+// fold: a batch without NaNs and zeros folds as unsigned min / max of monotone 16-bit
+// keys (two channels per instruction), any other batch element by element with
+// torch.minimum / maximum semantics.  A row outside the buffer is not folded (its load
+// reads row 0).
+template <int B, int PPW>
+__global__ __launch_bounds__(kThreads) void prefill_bounds_wave_kernel(PrefillArgs a) {
+  constexpr int C = 512;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t page0 = ((int64_t)blockIdx.x * (kThreads / 64) + wave) * PPW;
+  const int li = blockIdx.y;
+  const int layer = a.layer_begin + li;
+  if (a.set_counters && page0 == 0 && li == a.n_layers - 1 && lane == 0) {
+    a.count[a.req] = (int32_t)(a.n - a.full_pages * a.P);
+    a.page_idx[a.req] = (int32_t)a.full_pages;
+  }
+  if (page0 * a.P >= a.n) return;  // wave-uniform
+  const uint4* kl = reinterpret_cast<const uint4*>(a.k_base + (int64_t)li * a.k_layer_stride_bytes);
+  auto chunk_row = [&](int64_t t0, int cnt) -> int32_t {  // lane r: row t0 + r (-1: none)
+    int64_t r = lane < cnt ? load_index(a.idx, a.idx64, t0 + lane) : -1;
+    return (int32_t)((r >= 0 && r < a.k_rows) ? r : -1);  // rows < 2^31 (checked by the host)
+  };
+  int32_t first[PPW];
+#pragma unroll
+  for (int j = 0; j < PPW; ++j) {
+    const int64_t begin = (page0 + j) * a.P;
+    first[j] = chunk_row(begin, (int)max((int64_t)0, min((int64_t)min(a.P, 64), a.n - begin)));
+  }
+#pragma unroll
+  for (int j = 0; j < PPW; ++j) {
+    const int64_t page = page0 + j;
+    const int64_t begin = page * a.P;
+    const int64_t end = min(begin + (int64_t)a.P, a.n);
+    if (begin >= end) break;  // wave-uniform
+    // the fold so far as keys of channel pairs (8l + 2q, 8l + 2q + 1): +inf / -inf
+    uint32_t kmn[4], kmx[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      kmn[q] = 0xFF80FF80u;
+      kmx[q] = 0x007F007Fu;
+    }
+    for (int64_t t0 = begin; t0 < end && a.k_rows > 0; t0 += 64) {  // no rows: sentinels
+      const int cnt = (int)min((int64_t)64, end - t0);
+      const int32_t row32 = t0 == begin ? first[j] : chunk_row(t0, cnt);
+      for (int tb = 0; tb < cnt; tb += B) {  // wave-uniform
+        uint4 v[B];
+        bool ok[B];
+#pragma unroll
+        for (int i = 0; i < B; ++i) {
+          const int t = tb + i;
+          const int r = t < cnt ? __builtin_amdgcn_readlane(row32, t) : -1;
+          ok[i] = r >= 0;
+          v[i] = kl[(int64_t)(ok[i] ? r : 0) * (C / 8) + lane];
+        }
+        uint32_t sp = 0;  // a NaN or a zero in the batch, or a NaN already folded (it must stay)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          sp = u16x2_max(sp, u16x2_max(bf16x2_special(bf16x2_unkey(kmn[q])), bf16x2_special(bf16x2_unkey(kmx[q]))));
+#pragma unroll
+        for (int i = 0; i < B; ++i) {
+          if (!ok[i]) continue;  // wave-uniform
+          sp = u16x2_max(sp, u16x2_max(u16x2_max(bf16x2_special(v[i].x), bf16x2_special(v[i].y)),
+                                       u16x2_max(bf16x2_special(v[i].z), bf16x2_special(v[i].w))));
+        }
+        const bool special = (sp & 0xFFFFu) >= 0x7F80u || (sp >> 16) >= 0x7F80u;
+        if (!__builtin_amdgcn_ballot_w64(special)) {
+          // no NaN and no zero in the batch or the fold so far: unsigned min / max of the keys
+#pragma unroll
+          for (int i = 0; i < B; ++i) {
+            if (!ok[i]) continue;
+            const uint32_t w[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const uint32_t kw = bf16x2_key(w[q]);
+              kmn[q] = u16x2_min(kmn[q], kw);
+              kmx[q] = u16x2_max(kmx[q], kw);
+            }
+          }
+        } else {
+          // NaNs or zeros: torch.minimum / maximum element by element, in row order
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const uint32_t bmn = bf16x2_unkey(kmn[q]), bmx = bf16x2_unkey(kmx[q]);
+            uint16_t mn0 = (uint16_t)bmn, mn1 = (uint16_t)(bmn >> 16);
+            uint16_t mx0 = (uint16_t)bmx, mx1 = (uint16_t)(bmx >> 16);
+#pragma unroll
+            for (int i = 0; i < B; ++i) {
+              if (!ok[i]) continue;
+              const uint32_t w = q == 0 ? v[i].x : q == 1 ? v[i].y : q == 2 ? v[i].z : v[i].w;
+              mn0 = bmin(mn0, (uint16_t)w);
+              mn1 = bmin(mn1, (uint16_t)(w >> 16));
+              mx0 = bmax(mx0, (uint16_t)w);
+              mx1 = bmax(mx1, (uint16_t)(w >> 16));
+            }
+            kmn[q] = bf16x2_key((uint32_t)mn0 | ((uint32_t)mn1 << 16));
+            kmx[q] = bf16x2_key((uint32_t)mx0 | ((uint32_t)mx1 << 16));
+          }
+        }
+      }
+    }
+    uint16_t mn[8], mx[8];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t bmn = bf16x2_unkey(kmn[q]), bmx = bf16x2_unkey(kmx[q]);
+      mn[2 * q] = (uint16_t)bmn;
+      mn[2 * q + 1] = (uint16_t)(bmn >> 16);
+      mx[2 * q] = (uint16_t)bmx;
+      mx[2 * q + 1] = (uint16_t)(bmx >> 16);
+    }
+    const int c0 = lane * 8;
+    if (page < a.full_pages) {
+      if (page < a.MP) {
+        uint32_t* dst = a.bounds + (((int64_t)layer * a.R + a.req) * a.MP + page) * C + c0;
+        uint4 lo, hi;
+        lo.x = pack_pair(mn[0], mx[0]);
+        lo.y = pack_pair(mn[1], mx[1]);
+        lo.z = pack_pair(mn[2], mx[2]);
+        lo.w = pack_pair(mn[3], mx[3]);
+        hi.x = pack_pair(mn[4], mx[4]);
+        hi.y = pack_pair(mn[5], mx[5]);
+        hi.z = pack_pair(mn[6], mx[6]);
+        hi.w = pack_pair(mn[7], mx[7]);
+        reinterpret_cast<uint4*>(dst)[0] = lo;
+        reinterpret_cast<uint4*>(dst)[1] = hi;
+      }
+    } else {
+      const int64_t rc = ((int64_t)layer * a.R + a.req) * C + c0;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        a.rmin[rc + e] = mn[e];
+        a.rmax[rc + e] = mx[e];
+      }
     }
   }
 }
@@ -440,6 +603,9 @@ extern "C" int qq_quest_prefill_bounds(const void* k_base, int64_t k_layer_strid
                     k_layer_stride % 8 == 0 && reinterpret_cast<uintptr_t>(k_base) % 16 == 0;
   if (!wide)
     prefill_bounds_kernel<<<grid, kThreads, 0, s>>>(a);
+  else if (C == 512 && k_rows <= INT32_MAX)
+    prefill_bounds_wave_kernel<kWaveFoldBatch, kWavePages>
+        <<<dim3(ceil_div(pages, kThreads / 64 * kWavePages), n_layers), kThreads, 0, s>>>(a);
   else if (C == 512)
     prefill_bounds_wide_kernel<64><<<grid, kThreads, 0, s>>>(a);
   else if (C == 1024)

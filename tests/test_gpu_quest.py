@@ -60,15 +60,43 @@ def test_init_storage_sentinels_match_oracle():
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("n", [0, 30, 64, 192, 200, 777])
-def test_prefill_bounds_bit_exact(dtype, n):
-    q, st = new_quest(256, 64, 2, 4, 1024, 4, 32)
-    pool = rand_bf16((1100, 4, 32), seed=n).to(dtype)
-    idx = torch.randperm(1100, generator=torch.Generator().manual_seed(1))[:n].to(torch.int32)
+@pytest.mark.parametrize("d,idx_dtype", [(32, torch.int32), (128, torch.int32), (128, torch.int64)])
+def test_prefill_bounds_bit_exact(dtype, n, d, idx_dtype):
+    """KV*D = 128 (the 16-byte block fold), 512 (one wave per page, bf16), fp32 keys (the
+    per-element fold); partial pages, gathered rows, int32 and int64 indices."""
+    q, st = new_quest(256, 64, 2, 4, 1024, 4, d)
+    pool = rand_bf16((1100, 4, d), seed=n).to(dtype)
+    idx = torch.randperm(1100, generator=torch.Generator().manual_seed(1))[:n].to(idx_dtype)
     host = pool.float().numpy() if dtype == torch.float32 else bf16_bits(pool)
     for layer in range(2):
         q.update_prefill_representations(layer, 2, pool.to(DEV), idx.to(DEV))
         st.update_prefill_representations(layer, 2, host, idx.numpy())
     assert_state_equal(q, st)
+
+
+def test_prefill_bounds_special_values_fold_in_row_order():
+    """bf16 keys at KV*D = 512 (one wave per page: batches without NaN or zero fold as
+    16-bit key min / max, the others element by element) against the same keys as fp32
+    (the per-element fold): NaN, +-0 and +-inf scattered over the rows, bit-identical
+    bounds and running bounds."""
+    n, d = 777, 128
+    pool = rand_bf16((1100, 4, d), seed=5)
+    bits = pool.view(torch.int16)
+    g = torch.Generator().manual_seed(6)
+    for val in (0x7FC0, 0x0000, 0x8000, 0x7F80, 0xFF80):
+        for _ in range(25):
+            r = int(torch.randint(0, 1100, (1,), generator=g))
+            c = int(torch.randint(0, 4 * d, (1,), generator=g))
+            bits[r].view(-1)[c] = val - 65536 if val >= 32768 else val
+    idx = torch.randperm(1100, generator=torch.Generator().manual_seed(1))[:n].to(torch.int32)
+    qb, _ = new_quest(256, 64, 1, 4, 1024, 4, d)
+    qf, _ = new_quest(256, 64, 1, 4, 1024, 4, d)
+    qb.update_prefill_representations(0, 2, pool.to(DEV), idx.to(DEV))
+    qf.update_prefill_representations(0, 2, pool.float().to(DEV), idx.to(DEV))
+    torch.cuda.synchronize()
+    for name in ("page_k_bounds", "running_k_min", "running_k_max"):
+        assert torch.equal(getattr(qb, name).view(torch.int16), getattr(qf, name).view(torch.int16)), name
+    assert torch.isnan(qb.page_k_bounds.float()).any()
 
 
 def test_prefill_fused_over_layers_equals_per_layer():
