@@ -207,24 +207,35 @@ __device__ inline void finish_block(const StepArgs& a, int bh, int part, float M
   __syncthreads();
   uint16_t* outp = a.out + (int64_t)b * sa.H * kMfmaDim + (int64_t)h * G * kMfmaDim;
   const int64_t part_idx = (int64_t)bh * parts + part;
-  for (int idx = tid; idx < G * kMfmaDim; idx += kThreads) {
-    const int head = idx >> 7, d = idx & 127;
+  const __amdgpu_buffer_rsrc_t po =
+      agent_rsrc(a.part_o + part_idx * G * kMfmaDim, (uint32_t)(G * kMfmaDim * sizeof(float)));
+  // each thread one head x 4 channels: the waves' (m, l, o) weighted in wave order
+  for (int grp = tid; grp < G * (kMfmaDim / 4); grp += kThreads) {
+    const int head = grp >> 5, d4 = (grp & 31) * 4;
     float Mx = -INFINITY;
 #pragma unroll
     for (int w = 0; w < W; ++w) Mx = fmaxf(Mx, sm_m[w][head]);
-    float Ls = 0.0f, Os = 0.0f;
+    float Ls = 0.0f;
+    float4 Os = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
     for (int w = 0; w < W; ++w) {
       const float mw = sm_m[w][head];
       const float wgt = mw == -INFINITY ? 0.0f : exp2f(mw - Mx);
       Ls += wgt * sm_l[w][head];
-      Os += wgt * sm_o[w][head][d];
+      const float4 ov = *reinterpret_cast<const float4*>(&sm_o[w][head][d4]);
+      Os.x += wgt * ov.x;
+      Os.y += wgt * ov.y;
+      Os.z += wgt * ov.z;
+      Os.w += wgt * ov.w;
     }
     if (parts == 1) {
-      outp[idx] = f2bf(!(Ls <= 0.0f) ? Os / Ls : 0.0f);  // NaN (a poisoned part) stays NaN
+      const bool any = !(Ls <= 0.0f);  // NaN (a poisoned part) stays NaN
+      const uint32_t lo2 = (uint32_t)f2bf(any ? Os.x / Ls : 0.0f) | ((uint32_t)f2bf(any ? Os.y / Ls : 0.0f) << 16);
+      const uint32_t hi2 = (uint32_t)f2bf(any ? Os.z / Ls : 0.0f) | ((uint32_t)f2bf(any ? Os.w / Ls : 0.0f) << 16);
+      *reinterpret_cast<uint2*>(outp + head * kMfmaDim + d4) = make_uint2(lo2, hi2);
     } else {
-      st_agent(a.part_o + (part_idx * G + head) * kMfmaDim + d, Os);
-      if (d == 0) {
+      st_agent_x4(po, (uint32_t)((head * kMfmaDim + d4) * sizeof(float)), Os);
+      if (d4 == 0) {
         st_agent(a.part_ml + (part_idx * G + head) * 2, Mx);
         st_agent(a.part_ml + (part_idx * G + head) * 2 + 1, Ls);
       }

@@ -53,8 +53,9 @@ __device__ inline void wait_memory() { __asm__ volatile("s_waitcnt vmcnt(0)" :::
 // stay in flight across it; uses of their results get their own waits.
 __device__ inline void lds_barrier() { __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-// 16-byte agent-scope loads through a buffer resource (cache policy sc1, as
-// the agent-scope loads above use); offsets past `bytes` read zeros.
+// 16-byte agent-scope loads and stores through a buffer resource (cache policy
+// sc1, as the agent-scope accesses above use); offsets past `bytes` read zeros
+// (and are not written).
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 constexpr int kCachePolicyAgent = 16;  // sc1
 __device__ inline __amdgpu_buffer_rsrc_t agent_rsrc(const void* base, uint32_t bytes) {
@@ -63,6 +64,10 @@ __device__ inline __amdgpu_buffer_rsrc_t agent_rsrc(const void* base, uint32_t b
 __device__ inline float4 ld_agent_x4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
   const u32x4_t u = __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, 0, kCachePolicyAgent);
   return make_float4(__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z), __uint_as_float(u.w));
+}
+__device__ inline void st_agent_x4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, float4 v) {
+  const u32x4_t u = {__float_as_uint(v.x), __float_as_uint(v.y), __float_as_uint(v.z), __float_as_uint(v.w)};
+  __builtin_amdgcn_raw_buffer_store_b128(u, r, (int)byte_off, 0, kCachePolicyAgent);
 }
 
 // ------------------------------------------------------------------ new token
