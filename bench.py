@@ -201,14 +201,6 @@ def hisparse_measure(B: int, S: int, L: int, warmup: int, steps: int, event_step
     be.on_extend_finished(pre)
     torch.cuda.synchronize()
     setup_s = time.perf_counter() - t_setup
-    prefill = None
-    if B > 1:
-        pf_us = pf0.elapsed_time(pf1) * 1e3
-        pf_bytes = float(sum(int(c) - 1 for c in ctxs[1:])) * L * KV * D * 2  # every prompt key read once
-        prefill = {"kernel": "prefill_bounds_wave_kernel", "requests": B - 1, "layers": L,
-                   "tokens_per_request": int(ctxs[1:].mean()) - 1, "us_per_request": round(pf_us / (B - 1), 1),
-                   "gbs": round(pf_bytes / (pf_us * 1e-6) / 1e9, 1),
-                   "hbm_frac": round(pf_bytes / (pf_us * 1e-6) / (HBM_PEAK_GBS * 1e9), 4)}
 
     coord = be.coord
     layers = [Layer(i, D**-0.5) for i in range(L)]
@@ -352,14 +344,6 @@ def dense_bench(args) -> int:
     batch = ForwardBatch(ForwardMode.DECODE, None, None, torch.arange(B, device=dev), seq_lens, out_loc, rtp, kvp, be)
     torch.cuda.synchronize()
     setup_s = time.perf_counter() - t_setup
-    prefill = None
-    if B > 1:
-        pf_us = pf0.elapsed_time(pf1) * 1e3
-        pf_bytes = float(sum(int(c) - 1 for c in ctxs[1:])) * L * KV * D * 2  # every prompt key read once
-        prefill = {"kernel": "prefill_bounds_wave_kernel", "requests": B - 1, "layers": L,
-                   "tokens_per_request": int(ctxs[1:].mean()) - 1, "us_per_request": round(pf_us / (B - 1), 1),
-                   "gbs": round(pf_bytes / (pf_us * 1e-6) / 1e9, 1),
-                   "hbm_frac": round(pf_bytes / (pf_us * 1e-6) / (HBM_PEAK_GBS * 1e9), 4)}
 
     def step():
         torch.add(base, seq_lens - 1, out=out_loc)
