@@ -169,14 +169,17 @@ def pinned_h2d_peak(nbytes: int = 1 << 30, reps: int = 5) -> float:
     return nbytes * reps / (e0.elapsed_time(e1) * 1e-3) / 1e9
 
 
-def hisparse_measure(B: int, S: int, L: int, warmup: int, steps: int, event_steps: int) -> dict:
+def hisparse_measure(B: int, S: int, L: int, warmup: int, steps: int, event_steps: int, route: str = "kernel") -> dict:
     """quest_hisparse decode (QuestHiSparseBackend, the drop-in path) at batch B x S tokens, a
     hot buffer of 4096 + 1 rows per request and layer, the K/V history of L layers in pinned
     host memory, queries AR(1) with rho 0.9 across steps.  After `warmup` eager steps, one
     decode step (bounds fold + eager backup + per layer new token, selection, swap-in and
     attention) is captured in a HIP graph and replayed for `steps` timed steps (µs per
     layer-step); `event_steps` more steps run eagerly with HIP events around every swap-in
-    call (plan + copy) on the launch stream, for the swap-in time and the missed rows."""
+    call (plan + copy) on the launch stream, for the swap-in time and the missed rows.
+    route "memcpy": the swap-in's copy through the copy engines (QuestHiSparseBackend
+    swap_route="memcpy": a host synchronisation per swap-in, so no graph; the `steps` timed
+    steps run eagerly with HIP events around each step)."""
     from qwenquest_amd.attention.quest_hisparse import QuestHiSparseBackend
     from qwenquest_amd.batch import ForwardBatch, ForwardMode
     from qwenquest_amd.memory import MHATokenToKVPool, ReqToTokenPool
@@ -195,7 +198,7 @@ def hisparse_measure(B: int, S: int, L: int, warmup: int, steps: int, event_step
     base = 1 + torch.arange(B, device=dev, dtype=torch.int64) * max_ctx
     rtp.req_to_token.copy_((base[:, None] + torch.arange(max_ctx, device=dev)[None]).to(torch.int32))
     be = QuestHiSparseBackend(rtp, kvp, {"algorithm": "quest", "top_k": TOP_K, "quest_page_size": P,
-                                         "device_buffer_size": BUF}, host_pool_size=B * max_ctx)
+                                         "device_buffer_size": BUF}, host_pool_size=B * max_ctx, swap_route=route)
     prompt = S - 1
     pre = ForwardBatch(ForwardMode.EXTEND, None, None, torch.arange(B), torch.full((B,), prompt), None, rtp, kvp, be)
     be.on_extend_finished(pre)
@@ -225,9 +228,12 @@ def hisparse_measure(B: int, S: int, L: int, warmup: int, steps: int, event_step
         step()
         seq.add_(1)
     torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        step()
+    use_graph = route == "kernel"
+    graph = None
+    if use_graph:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step()
     stream = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     step_ms = []
@@ -235,7 +241,10 @@ def hisparse_measure(B: int, S: int, L: int, warmup: int, steps: int, event_step
     for _ in range(steps):
         next_inputs()
         e0.record(stream)
-        graph.replay()
+        if use_graph:
+            graph.replay()
+        else:
+            step()
         e1.record(stream)
         e1.synchronize()
         step_ms.append(e0.elapsed_time(e1))
@@ -273,7 +282,8 @@ def hisparse_measure(B: int, S: int, L: int, warmup: int, steps: int, event_step
     st = coord.stats
     res = {
         "us_per_layer_step": round(float(np.mean(step_ms)) * 1e3 / L, 2),
-        "graph": True,
+        "graph": use_graph,
+        "swap_route": route,
         "swap_in_rows_per_layer_step": round(miss_rows, 1),
         "graph_swap_in_rows_per_layer_step": round(graph_misses / steps / L, 1),
         "swap_in_us_per_layer_step": round(swap_us, 2),
@@ -284,8 +294,9 @@ def hisparse_measure(B: int, S: int, L: int, warmup: int, steps: int, event_step
         "hit_rate": round(st.hit_rate, 4),
         "workload": f"quest_hisparse decode, batch {B}, {S}-token context, hot buffer {BUF}+1 rows, {L} layers' "
                     f"history in pinned host memory (the per-layer work is the same for all 48), AR(1) queries "
-                    f"rho 0.9; {warmup} warm-up steps, {steps} graph-replayed timed steps, {event_steps} eager "
-                    f"steps with events around the swap-in",
+                    f"rho 0.9; {warmup} warm-up steps, {steps} {'graph-replayed' if use_graph else 'eager'} timed "
+                    f"steps, {event_steps} eager steps with events around the swap-in; swap-in copy: "
+                    f"{'copy kernel reading pinned host memory' if use_graph else 'hipMemcpyAsync per run of host rows on a side stream + scatter'}",
         "setup_s": round(setup_s, 1),
     }
     del be, coord, kvp, rtp, graph
@@ -295,7 +306,8 @@ def hisparse_measure(B: int, S: int, L: int, warmup: int, steps: int, event_step
 
 def hisparse_bench(args) -> int:
     torch.cuda.set_device(0)
-    r = hisparse_measure(args.batch, args.ctx, args.hisparse_layers, args.warmup, args.steps, args.steps)
+    r = hisparse_measure(args.batch, args.ctx, args.hisparse_layers, args.warmup, args.steps, args.steps,
+                         route=args.hisparse_route)
     print(json.dumps({
         "metric": "quest_hisparse decode @128K ctx, batch 16: swap-in H2D GB/s and us per layer-step",
         "value": r["h2d_gbs"], "unit": "GB/s (swap-in misses x 2 KiB / swap-in time)",
@@ -402,6 +414,8 @@ def main() -> int:
                     help="contexts drawn uniform in [8192, ctx] per request (seeded) instead of all ctx")
     ap.add_argument("--hisparse", action="store_true", help="measure the quest_hisparse tier instead")
     ap.add_argument("--hisparse-layers", type=int, default=4)
+    ap.add_argument("--hisparse-route", choices=("kernel", "memcpy"), default="kernel",
+                    help="--hisparse: the swap-in's host -> device copy (memcpy: hipMemcpyAsync per run on a side stream)")
     ap.add_argument("--hisparse-steps", type=int, default=48,
                     help="graph-replayed quest_hisparse steps measured after the headline (0 = skip)")
     ap.add_argument("--dense", action="store_true",

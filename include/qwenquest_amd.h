@@ -321,6 +321,22 @@ int qq_hisparse_swap_in(const int32_t* positions, int64_t positions_stride,
                         int64_t* copy_src, int32_t* copy_count, uint64_t* stats,
                         int32_t* error_flags, int32_t* error_mirror, void* stream);
 
+/* qq_hisparse_swap_in without its copy: the plan only (rows_out, buffer_tokens,
+ * lru_slots, stats and errors as there); the layer's misses are left in
+ * copy_dst / copy_src [bs, top_k] (hot-buffer row <- host row, copy_count[b] of
+ * them per request) for the caller to copy.  Serves the swap-in route the
+ * reference's upstream takes (coordinator.py:282-291: pinned-host
+ * hipMemcpyAsync on a side stream), which the coordinator offers as
+ * swap_route="memcpy" to measure it against the in-kernel copy. */
+int qq_hisparse_swap_plan(const int32_t* positions, int64_t positions_stride,
+                          const int32_t* actual_lens, const int64_t* seq_lens,
+                          const int64_t* req_pool_indices, int bs, int max_reqs,
+                          int device_buffer_size, int top_k, int64_t* buffer_tokens_layer,
+                          int64_t* lru_slots_layer, const int64_t* req_to_host_pool,
+                          int64_t max_context_len, int64_t* rows_out, int64_t* copy_dst,
+                          int64_t* copy_src, int32_t* copy_count, uint64_t* stats,
+                          int32_t* error_flags, int32_t* error_mirror, void* stream);
+
 /* Row copies over n_layers layers: dst[layer][dst_idx[i]] = src[layer][src_idx[i]]
  * (row_bytes each; indices outside [0, rows) are skipped).  Carries the
  * admission copies (coordinator.py:158-164: token pool -> host tier and hot

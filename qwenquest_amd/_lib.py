@@ -84,6 +84,10 @@ SIGNATURES: dict[str, tuple] = {
         [_P, _L, _P, _P, _P, _I, _I, _I, _I, _P, _P, _P, _L, _P, _P, _P, _P, _L, _L, _P, _P, _P,
          _P, _P, _P, _P, _P],
     ),
+    "qq_hisparse_swap_plan": (
+        _I,
+        [_P, _L, _P, _P, _P, _I, _I, _I, _I, _P, _P, _P, _L, _P, _P, _P, _P, _P, _P, _P, _P],
+    ),
     "qq_copy_rows": (_I, [_P, _L, _L, _P, _P, _L, _L, _P, _I, _I, _L, _P]),
     "qq_hisparse_request_state": (_I, [_P, _P, _I, _I, _I, _P, _L, _I, _P, _L, _I, _P]),
     "qq_hisparse_backup_step": (_I, [_P, _P, _I, _P, _I, _I, _P, _L, _P, _P, _L, _P, _P, _P, _P, _P]),

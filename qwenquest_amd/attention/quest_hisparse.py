@@ -46,6 +46,7 @@ class QuestHiSparseBackend(AttentionBackend):
         start_layer: int = 0,
         end_layer: int | None = None,
         host_device: torch.device | str = "cpu",
+        swap_route: str = "kernel",
     ):
         super().__init__(req_to_token_pool, token_to_kv_pool)
         cfg = parse_hisparse_config(sparse_config)
@@ -79,6 +80,7 @@ class QuestHiSparseBackend(AttentionBackend):
             dtype=token_to_kv_pool.dtype,
             device=device,
             host_device=host_device,
+            swap_route=swap_route,
         )
         self._positions = torch.empty((req_to_token_pool.size, cfg.top_k), dtype=torch.int32, device=device)
         self._attn_ws = AttentionWorkspace(device)

@@ -696,18 +696,15 @@ static int plan_lds_opt_in() {
   return QQ_OK;
 }
 
-extern "C" int qq_hisparse_swap_in(const int32_t* positions, int64_t positions_stride,
-                                   const int32_t* actual_lens, const int64_t* seq_lens,
-                                   const int64_t* req_pool_indices, int bs, int max_reqs,
-                                   int device_buffer_size, int top_k, int64_t* buffer_tokens_layer,
-                                   int64_t* lru_slots_layer, const int64_t* req_to_host_pool,
-                                   int64_t max_context_len, void* device_k_layer,
-                                   void* device_v_layer, const void* host_k_layer,
-                                   const void* host_v_layer, int64_t row_bytes,
-                                   int64_t host_rows, int64_t* rows_out, int64_t* copy_dst,
-                                   int64_t* copy_src, int32_t* copy_count, uint64_t* stats,
-                                   int32_t* error_flags, int32_t* error_mirror, void* stream) {
-  const char* what = "qq_hisparse_swap_in";
+// The swap-in of one layer: the plan, then (copy) the misses' host -> device copy.
+static int swap_in(const char* what, bool copy, const int32_t* positions, int64_t positions_stride,
+                   const int32_t* actual_lens, const int64_t* seq_lens, const int64_t* req_pool_indices, int bs,
+                   int max_reqs, int device_buffer_size, int top_k, int64_t* buffer_tokens_layer,
+                   int64_t* lru_slots_layer, const int64_t* req_to_host_pool, int64_t max_context_len,
+                   void* device_k_layer, void* device_v_layer, const void* host_k_layer, const void* host_v_layer,
+                   int64_t row_bytes, int64_t host_rows, int64_t* rows_out, int64_t* copy_dst, int64_t* copy_src,
+                   int32_t* copy_count, uint64_t* stats, int32_t* error_flags, int32_t* error_mirror,
+                   void* stream) {
   QQ_REQUIRE(bs >= 0 && max_reqs > 0 && device_buffer_size >= top_k && top_k > 0,
              "%s: bad sizes (buf %d, top_k %d)", what, device_buffer_size, top_k);
   QQ_REQUIRE(device_buffer_size <= kMaxPerThread * kPlanThreads && top_k <= kMaxPerThread * kPlanThreads,
@@ -763,8 +760,40 @@ extern "C" int qq_hisparse_swap_in(const int32_t* positions, int64_t positions_s
     swap_plan_kernel<kSmallEntries, kSmallSlots><<<bs, kPlanThreads, smem, s>>>(a);
   else
     swap_plan_kernel<kMaxPerThread, kMaxPerThread><<<bs, kPlanThreads, smem, s>>>(a);
-  swap_copy_kernel<<<dim3((top_k + kCopyRowsPerBlock - 1) / kCopyRowsPerBlock, bs), kCopyWaves * 64, 0, s>>>(a);
+  if (copy)
+    swap_copy_kernel<<<dim3((top_k + kCopyRowsPerBlock - 1) / kCopyRowsPerBlock, bs), kCopyWaves * 64, 0, s>>>(a);
   return check_launch(what);
+}
+
+extern "C" int qq_hisparse_swap_in(const int32_t* positions, int64_t positions_stride,
+                                   const int32_t* actual_lens, const int64_t* seq_lens,
+                                   const int64_t* req_pool_indices, int bs, int max_reqs,
+                                   int device_buffer_size, int top_k, int64_t* buffer_tokens_layer,
+                                   int64_t* lru_slots_layer, const int64_t* req_to_host_pool,
+                                   int64_t max_context_len, void* device_k_layer,
+                                   void* device_v_layer, const void* host_k_layer,
+                                   const void* host_v_layer, int64_t row_bytes,
+                                   int64_t host_rows, int64_t* rows_out, int64_t* copy_dst,
+                                   int64_t* copy_src, int32_t* copy_count, uint64_t* stats,
+                                   int32_t* error_flags, int32_t* error_mirror, void* stream) {
+  return swap_in("qq_hisparse_swap_in", true, positions, positions_stride, actual_lens, seq_lens, req_pool_indices,
+                 bs, max_reqs, device_buffer_size, top_k, buffer_tokens_layer, lru_slots_layer, req_to_host_pool,
+                 max_context_len, device_k_layer, device_v_layer, host_k_layer, host_v_layer, row_bytes, host_rows,
+                 rows_out, copy_dst, copy_src, copy_count, stats, error_flags, error_mirror, stream);
+}
+
+extern "C" int qq_hisparse_swap_plan(const int32_t* positions, int64_t positions_stride,
+                                     const int32_t* actual_lens, const int64_t* seq_lens,
+                                     const int64_t* req_pool_indices, int bs, int max_reqs,
+                                     int device_buffer_size, int top_k, int64_t* buffer_tokens_layer,
+                                     int64_t* lru_slots_layer, const int64_t* req_to_host_pool,
+                                     int64_t max_context_len, int64_t* rows_out, int64_t* copy_dst,
+                                     int64_t* copy_src, int32_t* copy_count, uint64_t* stats,
+                                     int32_t* error_flags, int32_t* error_mirror, void* stream) {
+  return swap_in("qq_hisparse_swap_plan", false, positions, positions_stride, actual_lens, seq_lens,
+                 req_pool_indices, bs, max_reqs, device_buffer_size, top_k, buffer_tokens_layer, lru_slots_layer,
+                 req_to_host_pool, max_context_len, nullptr, nullptr, nullptr, nullptr, 16, 0, rows_out, copy_dst,
+                 copy_src, copy_count, stats, error_flags, error_mirror, stream);
 }
 
 extern "C" int qq_copy_rows(const void* src, int64_t src_layer_stride_bytes, int64_t src_rows,

@@ -99,6 +99,7 @@ class HiSparseCoordinator:
         device: torch.device | str,
         host_device: torch.device | str = "cpu",
         sync_errors: bool = False,
+        swap_route: str = "kernel",
     ):
         # coordinator.py:91-94
         if device_buffer_size < top_k:
@@ -119,6 +120,14 @@ class HiSparseCoordinator:
         self.device_buffer_size = buf = device_buffer_size
         self.dtype = dtype
         self.sync_errors = sync_errors
+        # the swap-in's host -> device copy: "kernel" = the plan kernel's misses read by a copy
+        # kernel straight from pinned host memory (no host synchronisation, graph-capturable);
+        # "memcpy" = the misses' runs of consecutive host rows as hipMemcpyAsync on a side
+        # stream into a staging buffer, then a scatter (the upstream route of
+        # coordinator.py:282-291; the copy list is on the device, so each swap-in synchronises)
+        if swap_route not in ("kernel", "memcpy"):
+            raise ValueError(f"swap_route must be 'kernel' or 'memcpy', got {swap_route!r}")
+        self.swap_route = swap_route
         self.row_elems = kv_heads * head_dim
         self.row_bytes = self.row_elems * torch.tensor([], dtype=dtype).element_size()
 
@@ -153,6 +162,10 @@ class HiSparseCoordinator:
         self._err = torch.zeros(1, dtype=torch.int32, device=self.device)
         self._err_host = torch.zeros(4, dtype=torch.int32, pin_memory=True)
         self._err_host_dev = self._device_address(self._err_host)
+        if swap_route == "memcpy":
+            self._side = torch.cuda.Stream(self.device)
+            self._stage_k = torch.empty((max_reqs * top_k, kv_heads, head_dim), dtype=dtype, device=self.device)
+            self._stage_v = torch.empty_like(self._stage_k)
         # the eager backup's per-step state, on the device: first-step skip flags and the
         # host-row free list; persistent step buffers (graph capture)
         self._skip_first_backup = torch.zeros(max_reqs, dtype=torch.uint8, device=self.device)
@@ -308,6 +321,19 @@ class HiSparseCoordinator:
         actual = actual_lens if actual_lens is not None else seq.clamp(max=self.top_k).to(torch.int32)
         actual = actual.to(device=self.device, dtype=torch.int32).contiguous()
         rows = out if out is not None else torch.empty((bs, self.top_k), dtype=torch.int64, device=self.device)
+        if self.swap_route == "memcpy":
+            _lib.call(
+                "qq_hisparse_swap_plan", _lib.ptr(pos), pos.stride(0), _lib.ptr(actual), _lib.ptr(seq),
+                _lib.ptr(rpi), bs, self.max_reqs, self.device_buffer_size, self.top_k,
+                _lib.ptr(self.buffer_tokens[layer_id]), _lib.ptr(self.lru_slots[layer_id]),
+                _lib.ptr(self.req_to_host_pool), self.max_context_len, _lib.ptr(rows), _lib.ptr(self._copy_dst),
+                _lib.ptr(self._copy_src), _lib.ptr(self._copy_count), _lib.ptr(self._stats), _lib.ptr(self._err),
+                self._err_host_dev, _lib.stream(self.device),
+            )
+            self._copy_misses_memcpy(bs, layer_id)
+            if self.sync_errors:
+                self.check_errors()
+            return rows
         _lib.call(
             "qq_hisparse_swap_in", _lib.ptr(pos), pos.stride(0), _lib.ptr(actual), _lib.ptr(seq), _lib.ptr(rpi),
             bs, self.max_reqs, self.device_buffer_size, self.top_k, _lib.ptr(self.buffer_tokens[layer_id]),
@@ -321,6 +347,34 @@ class HiSparseCoordinator:
         if self.sync_errors:
             self.check_errors()
         return rows
+
+    def _copy_misses_memcpy(self, bs: int, layer_id: int) -> None:
+        """The planned misses of one layer through the copy engines: runs of consecutive host
+        rows as hipMemcpyAsync (pinned host -> staging) on a side stream, then one scatter of
+        the staged rows into their hot-buffer slots on the current stream."""
+        counts = self._copy_count[:bs].tolist()  # synchronises: the copy list is on the device
+        total = int(sum(counts))
+        if total == 0:
+            return
+        src = torch.cat([self._copy_src[b, :c] for b, c in enumerate(counts) if c > 0]).cpu()
+        dst = torch.cat([self._copy_dst[b, :c] for b, c in enumerate(counts) if c > 0])
+        cut = (torch.nonzero(src[1:] != src[:-1] + 1).flatten() + 1).tolist()
+        starts = [0] + cut
+        ends = cut + [total]
+        main = torch.cuda.current_stream(self.device)
+        self._side.wait_stream(main)  # the staging buffers' previous scatter has run
+        hk, hv = self.host_k_all[layer_id], self.host_v_all[layer_id]
+        with torch.cuda.stream(self._side):
+            for a, e in zip(starts, ends):
+                s0 = int(src[a])
+                self._stage_k[a:e].copy_(hk[s0 : s0 + e - a], non_blocking=True)
+                self._stage_v[a:e].copy_(hv[s0 : s0 + e - a], non_blocking=True)
+        main.wait_stream(self._side)
+        idx = torch.arange(total, dtype=torch.int64, device=self.device)
+        rows_dev = self.device_k[layer_id].shape[0]
+        for stage, dev in ((self._stage_k, self.device_k[layer_id]), (self._stage_v, self.device_v[layer_id])):
+            _lib.call("qq_copy_rows", _lib.ptr(stage), 0, total, _lib.ptr(idx), _lib.ptr(dev), 0, rows_dev,
+                      _lib.ptr(dst), total, 1, self.row_bytes, _lib.stream(self.device))
 
     # -------------------------------------------------- [H4] release
 

@@ -262,7 +262,8 @@ def test_quest_hisparse_is_bit_identical_to_quest(avoid, shape):
     """reference tests/test_engine.py:59-69 and test_bf16.py:27-43 at the backend boundary:
     the same q/k/v through QuestOnlyBackend and QuestHiSparseBackend over many decode steps
     (the hot buffer must swap) give bit-identical outputs and positions, also where quest
-    runs the fused layer step."""
+    runs the fused layer step; QuestHiSparseBackend with swap_route="memcpy" gives the same
+    bits and the same hot-buffer state as with the in-kernel copy."""
     from qwenquest_amd.attention.quest_hisparse import QuestHiSparseBackend
     from qwenquest_amd.attention.quest_only import QuestOnlyBackend
     from qwenquest_amd.batch import ForwardBatch, ForwardMode
@@ -277,14 +278,15 @@ def test_quest_hisparse_is_bit_identical_to_quest(avoid, shape):
     kk = torch.randn(L, 2, total, KVH, DIM, generator=gen).to(torch.bfloat16)
     vv = torch.randn(L, 2, total, KVH, DIM, generator=gen).to(torch.bfloat16)
     qq = torch.randn(steps, L, 2, H, DIM, generator=gen).to(torch.bfloat16)
-    outs, poss = {}, {}
-    for mode in ("quest", "quest_hisparse"):
+    outs, poss, stats = {}, {}, {}
+    for mode in ("quest", "quest_hisparse", "quest_hisparse_memcpy"):
         rtp = ReqToTokenPool(2, CTX, DEV)
         kvp = MHATokenToKVPool(2 * CTX, L, KVH, DIM, torch.bfloat16, DEV)
         if mode == "quest":
             be = QuestOnlyBackend(rtp, kvp, cfg)
         else:
-            be = QuestHiSparseBackend(rtp, kvp, cfg, host_pool_size=2 * CTX)
+            be = QuestHiSparseBackend(rtp, kvp, cfg, host_pool_size=2 * CTX,
+                                      swap_route="memcpy" if mode.endswith("memcpy") else "kernel")
         for r, n in prompts.items():
             rtp.req_to_token[r] = torch.arange(1 + r * CTX, 1 + (r + 1) * CTX, dtype=torch.int32)
             rows = torch.arange(1 + r * CTX, 1 + r * CTX + n)
@@ -314,14 +316,21 @@ def test_quest_hisparse_is_bit_identical_to_quest(avoid, shape):
                 res.append(be.forward_decode(qq[step, layer].to(DEV), kn, vn, Layer(layer), b).cpu())
                 pos.append(be._positions[:2].cpu())
         outs[mode], poss[mode] = torch.stack(res), torch.stack(pos)
-        if mode == "quest_hisparse":
+        if mode != "quest":
             st = be.coord.stats
             assert st.misses > 0 and st.hits > 0
+            stats[mode] = (st, be.coord.buffer_tokens.cpu(), be.coord.lru_slots.cpu(), be.coord.device_k_all.cpu())
     fused = _lib.load().qq_quest_fused_step(_lib.DTYPE_BF16, _lib.DTYPE_BF16, _lib.DTYPE_BF16, H, KVH, DIM, P, TOP_K,
                                             (CTX + P - 1) // P)
     assert fused == (shape == len(BIT_IDENTITY) - 1)
     assert torch.equal(poss["quest"], poss["quest_hisparse"])
     assert torch.equal(outs["quest"], outs["quest_hisparse"])
+    # the copy-engine swap-in route (plan kernel, hipMemcpyAsync per run of host rows on a side
+    # stream, scatter) leaves the same hot buffers and gives the same bits
+    assert torch.equal(poss["quest_hisparse_memcpy"], poss["quest_hisparse"])
+    assert torch.equal(outs["quest_hisparse_memcpy"], outs["quest_hisparse"])
+    a, b = stats["quest_hisparse"], stats["quest_hisparse_memcpy"]
+    assert a[0] == b[0] and all(torch.equal(x, y) for x, y in zip(a[1:], b[1:]))
 
 
 def test_device_row_allocator_hands_out_rows_in_the_reference_order():
