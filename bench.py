@@ -274,6 +274,7 @@ def hisparse_measure(B: int, S: int, L: int, warmup: int, steps: int, event_step
         misses.append(coord.stats.misses - m0)
         seq.add_(1)
     coord.swap_in_selected_pages = swap
+    cpu_plan = hisparse_cpu_baseline(coord, be, step, next_inputs, seq, B, TOP_K, BUF)
     row_bytes = 2 * KV * D * 2  # K + V row
     miss_rows = float(np.mean(misses)) / L
     swap_us = float(np.mean(swap_ms)) * 1e3 / L
@@ -292,6 +293,7 @@ def hisparse_measure(B: int, S: int, L: int, warmup: int, steps: int, event_step
         "h2d_frac_of_memcpy_peak": round(h2d / peak, 4) if peak > 0 else None,
         "h2d_frac_of_64gbs_nominal": round(h2d / 64.0, 4),
         "hit_rate": round(st.hit_rate, 4),
+        "cpu_baseline_swap_in": cpu_plan,
         "workload": f"quest_hisparse decode, batch {B}, {S}-token context, hot buffer {BUF}+1 rows, {L} layers' "
                     f"history in pinned host memory (the per-layer work is the same for all 48), AR(1) queries "
                     f"rho 0.9; {warmup} warm-up steps, {steps} {'graph-replayed' if use_graph else 'eager'} timed "
@@ -302,6 +304,71 @@ def hisparse_measure(B: int, S: int, L: int, warmup: int, steps: int, event_step
     del be, coord, kvp, rtp, graph
     torch.cuda.empty_cache()
     return res
+
+
+def hisparse_cpu_baseline(coord, be, step, next_inputs, seq, B: int, top_k: int, buf: int, reps: int = 20) -> dict:
+    """The reference's swap-in on the host (coordinator.py:232-304 restated in numpy:
+    oracle/hisparse.py's planner, then the misses' K and V rows copied host tier -> hot buffer
+    with numpy) for one layer-step: the B requests of layer 0 in one decode step, from the
+    state the GPU's swap-in started from (buffer_tokens, lru_slots, req_to_host_pool, the
+    selected positions), median of `reps` after 3 warm-ups on the host cores.  The planned
+    rows are checked against the GPU's."""
+    from oracle import hisparse as oh
+
+    cap = {}
+    swap = coord.swap_in_selected_pages
+
+    def capture(reqs, seqs, positions, layer_id, **kw):
+        if layer_id == 0 and not cap:
+            cap["tokens"] = coord.buffer_tokens[0].cpu().numpy().copy()
+            cap["lru"] = coord.lru_slots[0].cpu().numpy().copy()
+            cap["r2h"] = coord.req_to_host_pool.cpu().numpy()
+            cap["pos"] = positions.cpu().numpy().astype(np.int64)
+            cap["seq"] = seqs.cpu().numpy().astype(np.int64)
+            cap["reqs"] = reqs.cpu().numpy().astype(np.int64)
+            rows = swap(reqs, seqs, positions, layer_id, **kw)
+            cap["rows"] = rows.cpu().numpy().copy()
+            return rows
+        return swap(reqs, seqs, positions, layer_id, **kw)
+
+    coord.swap_in_selected_pages = capture
+    next_inputs()
+    step()
+    torch.cuda.synchronize()
+    seq.add_(1)
+    coord.swap_in_selected_pages = swap
+    host_k = coord.host_k_all[0].view(torch.int16).numpy()  # bf16 rows as raw 16-bit words
+    host_v = coord.host_v_all[0].view(torch.int16).numpy()
+    hot_k = np.empty((B * (buf + 1),) + host_k.shape[1:], dtype=host_k.dtype)
+    hot_v = np.empty_like(hot_k)
+
+    def plan_and_copy():
+        rows = np.full((B, top_k), -1, dtype=np.int64)
+        for b in range(B):
+            req, s = int(cap["reqs"][b]), int(cap["seq"][b])
+            n = min(s, top_k)
+            plan = oh.swap_in_long(cap["tokens"][req], cap["lru"][req], cap["pos"][b, :n], s, cap["r2h"][req])
+            base = req * (buf + 1)
+            rows[b, :n] = base + plan.slots
+            if plan.copies:
+                victims = base + np.array([c[0] for c in plan.copies])
+                hidx = np.array([c[1] for c in plan.copies])
+                hot_k[victims] = host_k[hidx]
+                hot_v[victims] = host_v[hidx]
+        return rows
+
+    for _ in range(3):
+        rows = plan_and_copy()
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        plan_and_copy()
+        times.append(time.perf_counter() - t0)
+    return {"value": round(float(np.median(times)) * 1e6, 1), "unit": "us per layer-step (16 requests' swap-in)",
+            "cores": 1, "kind": "port", "rows_equal_gpu": bool(np.array_equal(rows, cap["rows"])),
+            "sample": "one layer-step: the LRU planner of the reference (numpy restatement) and the misses' K/V "
+                      "row copies (numpy) for all requests of layer 0 in one decode step, from the GPU's state "
+                      f"before its swap-in; median of {reps} after 3 warm-ups, one thread"}
 
 
 def hisparse_bench(args) -> int:
