@@ -423,8 +423,7 @@ __device__ inline void attend_item(const StepArgs& a, int bh, int part, unsigned
       if (lo < G) {
         qb[ks] = *reinterpret_cast<const bf16x8_t*>(qp + ks * 32);
       } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) qb[ks][e] = (__bf16)0.0f;
+        qb[ks] = __builtin_bit_cast(bf16x8_t, u32x4_t{0u, 0u, 0u, 0u});
       }
     }
   }
@@ -536,8 +535,7 @@ __global__ __launch_bounds__(64 * W, 8 / W) void quest_attend_unit_kernel(StepAr
       if (lo < G) {
         qb[ks] = *reinterpret_cast<const bf16x8_t*>(qp + ks * 32);
       } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) qb[ks][e] = (__bf16)0.0f;
+        qb[ks] = __builtin_bit_cast(bf16x8_t, u32x4_t{0u, 0u, 0u, 0u});
       }
     }
   }

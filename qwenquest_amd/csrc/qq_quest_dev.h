@@ -612,8 +612,7 @@ __device__ inline void attn_wave64(const uint16_t* const* krow, const uint16_t* 
       if (lo < G) {
         qb[ks] = *reinterpret_cast<const bf16x8_t*>(qp + ks * 32);
       } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) qb[ks][e] = (__bf16)0.0f;
+        qb[ks] = __builtin_bit_cast(bf16x8_t, u32x4_t{0u, 0u, 0u, 0u});
       }
     }
   }
