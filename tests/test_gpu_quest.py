@@ -74,6 +74,19 @@ def test_prefill_bounds_bit_exact(dtype, n, d, idx_dtype):
     assert_state_equal(q, st)
 
 
+@pytest.mark.parametrize("page", [16, 128, 256])
+@pytest.mark.parametrize("n", [100, 777])
+def test_prefill_bounds_other_page_sizes_bit_exact(page, n):
+    """The wave-per-page fold at KV*D = 512 with pages shorter and longer than its 64-row index
+    chunks (bf16 keys, gathered rows, a partial last page)."""
+    q, st = new_quest(256, page, 1, 4, 1024, 4, 128)
+    pool = rand_bf16((1100, 4, 128), seed=n + page)
+    idx = torch.randperm(1100, generator=torch.Generator().manual_seed(2))[:n].to(torch.int32)
+    q.update_prefill_representations(0, 1, pool.to(DEV), idx.to(DEV))
+    st.update_prefill_representations(0, 1, bf16_bits(pool), idx.numpy())
+    assert_state_equal(q, st)
+
+
 def test_prefill_bounds_special_values_fold_in_row_order():
     """bf16 keys at KV*D = 512 (one wave per page: batches without NaN or zero fold as
     16-bit key min / max, the others element by element) against the same keys as fp32
