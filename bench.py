@@ -154,10 +154,13 @@ def cpu_baseline(be, q, batch, top_k: int, page: int, scaling: float, reps: int 
             "positions_equal_gpu": bool(same)}
 
 
-def pinned_h2d_peak(nbytes: int = 1 << 30, reps: int = 5) -> float:
-    """GB/s of hipMemcpy (torch copy) from pinned host memory into device memory."""
+def pinned_h2d_peak(nbytes: int = 1 << 30, reps: int = 5, d2h: bool = False) -> float:
+    """GB/s of hipMemcpy (torch copy) from pinned host memory into device memory (d2h: the
+    other way)."""
     src = torch.empty(nbytes, dtype=torch.uint8, pin_memory=True)
     dst = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    if d2h:
+        src, dst = dst, src
     dst.copy_(src, non_blocking=True)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -189,20 +192,31 @@ def hisparse_measure(B: int, S: int, L: int, warmup: int, steps: int, event_step
     total = warmup + steps + event_steps + 2
     max_ctx = S + total + 64
     t_setup = time.perf_counter()
-    rtp = ReqToTokenPool(B, max_ctx, dev)
-    kvp = MHATokenToKVPool(B * max_ctx, L, KV, D, torch.bfloat16, dev)
+    R = B + 1  # one more request slot: admitted while the B requests decode
+    rtp = ReqToTokenPool(R, max_ctx, dev)
+    kvp = MHATokenToKVPool(R * max_ctx, L, KV, D, torch.bfloat16, dev)
     gen = torch.Generator(device=dev).manual_seed(4321)
     for layer in range(L):
         kvp.k_all[layer].normal_(generator=gen)
         kvp.v_all[layer].normal_(generator=gen)
-    base = 1 + torch.arange(B, device=dev, dtype=torch.int64) * max_ctx
+    base = 1 + torch.arange(R, device=dev, dtype=torch.int64) * max_ctx
     rtp.req_to_token.copy_((base[:, None] + torch.arange(max_ctx, device=dev)[None]).to(torch.int32))
     be = QuestHiSparseBackend(rtp, kvp, {"algorithm": "quest", "top_k": TOP_K, "quest_page_size": P,
-                                         "device_buffer_size": BUF}, host_pool_size=B * max_ctx, swap_route=route)
+                                         "device_buffer_size": BUF}, host_pool_size=R * max_ctx, swap_route=route,
+                              async_admission=True)
     prompt = S - 1
     pre = ForwardBatch(ForwardMode.EXTEND, None, None, torch.arange(B), torch.full((B,), prompt), None, rtp, kvp, be)
-    be.on_extend_finished(pre)
+    # admission of the B prompts: K/V backup to the pinned host tier (device -> host over
+    # PCIe, on the admission stream), the first rows of the hot buffer, the bounds build
+    # (coordinator.py:138-174); timed until the backups are done
     torch.cuda.synchronize()
+    a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a0.record()
+    be.on_extend_finished(pre)
+    be.coord.wait_admission()
+    a1.record()
+    torch.cuda.synchronize()
+    admit_ms = a0.elapsed_time(a1)
     setup_s = time.perf_counter() - t_setup
 
     coord = be.coord
@@ -274,12 +288,47 @@ def hisparse_measure(B: int, S: int, L: int, warmup: int, steps: int, event_step
         misses.append(coord.stats.misses - m0)
         seq.add_(1)
     coord.swap_in_selected_pages = swap
+    overlap = None
+    if use_graph:
+        # one more request (slot B, a prompt of S-1 tokens) admitted while the B requests keep
+        # decoding: its backup runs on the admission stream, the decode graph on this one
+        torch.cuda.synchronize()
+        side = coord._adm_stream
+        b0, b1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        b0.record(side)
+        coord.admit_request(B, prompt, kvp, rtp.req_to_token[B, :prompt])
+        b1.record(side)
+        ends = []
+        for _ in range(16):
+            next_inputs()
+            s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s0.record(stream)
+            graph.replay()
+            s1.record(stream)
+            ends.append((s0, s1))
+            seq.add_(1)
+        torch.cuda.synchronize()
+        backup_ms = b0.elapsed_time(b1)
+        during = [a.elapsed_time(b) for a, b in ends if b0.elapsed_time(b) <= backup_ms]
+        coord.wait_admission(B)
+        overlap = {
+            "request_tokens": prompt,
+            "layers": L,
+            "backup_ms": round(backup_ms, 2),
+            "backup_d2h_gbs": round(prompt * L * 2 * KV * D * 2 / (backup_ms * 1e-3) / 1e9, 2),
+            "decode_steps_within_backup": len(during),
+            "decode_us_per_layer_step_within_backup": round(float(np.mean(during)) * 1e3 / L, 2) if during else None,
+            "decode_us_per_layer_step_alone": round(float(np.mean(step_ms)) * 1e3 / L, 2),
+        }
     cpu_plan = hisparse_cpu_baseline(coord, be, step, next_inputs, seq, B, TOP_K, BUF)
     row_bytes = 2 * KV * D * 2  # K + V row
     miss_rows = float(np.mean(misses)) / L
     swap_us = float(np.mean(swap_ms)) * 1e3 / L
     h2d = miss_rows * row_bytes / (swap_us * 1e-6) / 1e9 if swap_us > 0 else 0.0
     peak = pinned_h2d_peak()
+    d2h_peak = pinned_h2d_peak(d2h=True)
+    admit_bytes = B * prompt * L * row_bytes
+    admit_gbs = admit_bytes / (admit_ms * 1e-3) / 1e9
     st = coord.stats
     res = {
         "us_per_layer_step": round(float(np.mean(step_ms)) * 1e3 / L, 2),
@@ -294,6 +343,20 @@ def hisparse_measure(B: int, S: int, L: int, warmup: int, steps: int, event_step
         "h2d_frac_of_64gbs_nominal": round(h2d / 64.0, 4),
         "hit_rate": round(st.hit_rate, 4),
         "cpu_baseline_swap_in": cpu_plan,
+        "admission": {
+            "requests": B,
+            "tokens_per_request": prompt,
+            "layers": L,
+            "ms": round(admit_ms, 2),
+            "d2h_gbs": round(admit_gbs, 2),
+            "d2h_pinned_memcpy_peak_gbs": round(d2h_peak, 2),
+            "d2h_frac_of_memcpy_peak": round(admit_gbs / d2h_peak, 4) if d2h_peak > 0 else None,
+            "what": "on_extend_finished for the batch: every prompt's K and V rows backed up to the pinned host "
+                    "tier through the copy engines on the admission stream (the d2h bytes), the first hot-buffer "
+                    "rows and the page bounds built on the device, all inside the timed region; overlap: one more "
+                    "prompt admitted while the batch's decode graph is replayed",
+            "overlap": overlap,
+        },
         "workload": f"quest_hisparse decode, batch {B}, {S}-token context, hot buffer {BUF}+1 rows, {L} layers' "
                     f"history in pinned host memory (the per-layer work is the same for all 48), AR(1) queries "
                     f"rho 0.9; {warmup} warm-up steps, {steps} {'graph-replayed' if use_graph else 'eager'} timed "

@@ -47,6 +47,7 @@ class QuestHiSparseBackend(AttentionBackend):
         end_layer: int | None = None,
         host_device: torch.device | str = "cpu",
         swap_route: str = "kernel",
+        async_admission: bool = False,
     ):
         super().__init__(req_to_token_pool, token_to_kv_pool)
         cfg = parse_hisparse_config(sparse_config)
@@ -81,7 +82,11 @@ class QuestHiSparseBackend(AttentionBackend):
             device=device,
             host_device=host_device,
             swap_route=swap_route,
+            async_admission=async_admission,
         )
+        # with the admission backup on a side stream the prompt's pool rows are read after
+        # on_extend_finished returns: the engine frees them once coord.admission_done(req)
+        self.frees_prefill_kv_after_admission = not async_admission
         self._positions = torch.empty((req_to_token_pool.size, cfg.top_k), dtype=torch.int32, device=device)
         self._attn_ws = AttentionWorkspace(device)
         # QuestOnlyBackend runs its fused layer step for some shapes; the attention over the

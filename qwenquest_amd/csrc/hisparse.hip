@@ -461,18 +461,54 @@ __global__ __launch_bounds__(kCopyWaves * 64) void swap_copy_kernel(SwapArgs a) 
 }
 
 // Row copies for every layer: dst[layer][dst_row(i)] = src[layer][src_row(i)].
-// Rows whose index falls outside its buffer are skipped.
+// Rows whose index falls outside its buffer are skipped.  Grid-stride: each wave
+// moves kCopyRowsPerWave rows of one layer at a time (lane l: 16-byte chunks l,
+// l + 64, ... of each row), all their loads before their stores.
+constexpr int kCopyRowsPerWave = 4;
 __global__ __launch_bounds__(256) void copy_rows_kernel(const char* src, int64_t src_layer_stride,
                                                        int64_t src_rows, const int64_t* src_idx,
                                                        char* dst, int64_t dst_layer_stride,
                                                        int64_t dst_rows, const int64_t* dst_idx,
-                                                       int64_t row_bytes) {
-  const int i = blockIdx.x, layer = blockIdx.y;
-  const int64_t s = src_idx[i], d = dst_idx[i];
-  if (s < 0 || s >= src_rows || d < 0 || d >= dst_rows) return;
-  const uint4* sp = reinterpret_cast<const uint4*>(src + layer * src_layer_stride + s * row_bytes);
-  uint4* dp = reinterpret_cast<uint4*>(dst + layer * dst_layer_stride + d * row_bytes);
-  for (int64_t u = threadIdx.x; u < row_bytes / 16; u += 256) dp[u] = sp[u];
+                                                       int n, int n_layers, int64_t row_bytes) {
+  constexpr int R = kCopyRowsPerWave;
+  const int lane = threadIdx.x & 63;
+  const int64_t per_layer = ((int64_t)n + R - 1) / R;
+  const int64_t groups = per_layer * n_layers;
+  const int64_t waves = (int64_t)gridDim.x * (blockDim.x / 64);
+  const int64_t chunks = row_bytes / 16;
+  for (int64_t g = (int64_t)blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6); g < groups; g += waves) {
+    const int64_t layer = g / per_layer;
+    const int i0 = (int)(g - layer * per_layer) * R;
+    const uint4* sp[R];
+    uint4* dp[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int i = i0 + r;
+      const int64_t s = i < n ? src_idx[i] : -1, d = i < n ? dst_idx[i] : -1;
+      const bool ok = s >= 0 && s < src_rows && d >= 0 && d < dst_rows;
+      sp[r] = ok ? reinterpret_cast<const uint4*>(src + layer * src_layer_stride + s * row_bytes) : nullptr;
+      dp[r] = ok ? reinterpret_cast<uint4*>(dst + layer * dst_layer_stride + d * row_bytes) : nullptr;
+    }
+    for (int64_t c = lane; c < chunks; c += 64) {
+      uint4 v[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+        if (sp[r]) v[r] = sp[r][c];
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+        if (dp[r]) dp[r][c] = v[r];
+    }
+  }
+}
+
+// Whether `p` is host memory (pinned, addressed by the device over PCIe).
+static bool is_host_memory(const void* p) {
+  hipPointerAttribute_t attr;
+  if (hipPointerGetAttributes(&attr, p) != hipSuccess) {
+    (void)hipGetLastError();  // an unknown pointer: not host memory HIP knows of
+    return false;
+  }
+  return attr.type == hipMemoryTypeHost;
 }
 
 // Per-request bookkeeping: mode 0 = admit (tokens[s] = s, lru[s] = s, host rows of
@@ -803,9 +839,16 @@ extern "C" int qq_copy_rows(const void* src, int64_t src_layer_stride_bytes, int
   QQ_REQUIRE(n >= 0 && n_layers > 0 && row_bytes > 0 && row_bytes % 16 == 0,
              "qq_copy_rows: bad sizes");
   if (n == 0) return QQ_OK;
-  copy_rows_kernel<<<dim3(n, n_layers), 256, 0, static_cast<hipStream_t>(stream)>>>(
+  // Device copies: up to 1024 blocks of 4 waves (every CU busy, the copy at HBM rate).
+  // A large copy to or from pinned host memory is bound by PCIe, which 64 such blocks
+  // saturate (measured device -> host: 55 GB/s with 64 blocks or more); it then stays
+  // at 64 blocks, so kernels of other streams keep the rest of the chip while it runs.
+  const int64_t groups = ((int64_t)n + kCopyRowsPerWave - 1) / kCopyRowsPerWave * n_layers;
+  int64_t blocks = std::min<int64_t>((groups + 3) / 4, 1024);
+  if (blocks > 64 && groups >= 4096 && (is_host_memory(dst) || is_host_memory(src))) blocks = 64;
+  copy_rows_kernel<<<(int)blocks, 256, 0, static_cast<hipStream_t>(stream)>>>(
       static_cast<const char*>(src), src_layer_stride_bytes, src_rows, src_idx,
-      static_cast<char*>(dst), dst_layer_stride_bytes, dst_rows, dst_idx, row_bytes);
+      static_cast<char*>(dst), dst_layer_stride_bytes, dst_rows, dst_idx, n, n_layers, row_bytes);
   return check_launch("qq_copy_rows");
 }
 

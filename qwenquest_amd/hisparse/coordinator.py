@@ -100,6 +100,7 @@ class HiSparseCoordinator:
         host_device: torch.device | str = "cpu",
         sync_errors: bool = False,
         swap_route: str = "kernel",
+        async_admission: bool = False,
     ):
         # coordinator.py:91-94
         if device_buffer_size < top_k:
@@ -166,6 +167,18 @@ class HiSparseCoordinator:
             self._side = torch.cuda.Stream(self.device)
             self._stage_k = torch.empty((max_reqs * top_k, kv_heads, head_dim), dtype=dtype, device=self.device)
             self._stage_v = torch.empty_like(self._stage_k)
+        # admission's host backup (every prompt row's K and V to the pinned host tier: 2 KiB per
+        # token and layer over PCIe, the bulk of an admission) on a side stream when
+        # async_admission: the caller's stream goes on while it runs and waits for a request's
+        # backup (an event) only before a decode step of that request, before its release or
+        # before the request slot is admitted again.  The backup then goes through the copy
+        # engines (hipMemcpyAsync per run of rows consecutive in the pool and in the host
+        # tier): with a swap-in's copy kernel reading host memory at the same time, that
+        # kernel keeps its full host -> device rate (57 GB/s measured) and the backup gets
+        # ~30 GB/s; a backup by copy kernel took both to ~43 GB/s
+        self.async_admission = async_admission
+        self._adm_stream = torch.cuda.Stream(self.device) if async_admission else None
+        self._adm_pending: dict[int, torch.cuda.Event] = {}
         # the eager backup's per-step state, on the device: first-step skip flags and the
         # host-row free list; persistent step buffers (graph capture)
         self._skip_first_backup = torch.zeros(max_reqs, dtype=torch.uint8, device=self.device)
@@ -211,6 +224,57 @@ class HiSparseCoordinator:
 
     # -------------------------------------------------- [H1] admission
 
+    def admission_done(self, req_pool_idx: int) -> bool:
+        """Whether request ``req_pool_idx``'s admission backup has finished (no synchronisation;
+        always true without async_admission).  Its prompt rows in the token pool may be reused
+        only then."""
+        ev = self._adm_pending.get(int(req_pool_idx))
+        return ev is None or ev.query()
+
+    def wait_admission(self, req_pool_idx: int | None = None) -> None:
+        """Order the current stream after the admission backup of one request (all pending ones
+        for None); the host does not wait."""
+        reqs = list(self._adm_pending) if req_pool_idx is None else [int(req_pool_idx)]
+        cur = torch.cuda.current_stream(self.device)
+        for r in reqs:
+            ev = self._adm_pending.pop(r, None)
+            if ev is not None:
+                cur.wait_event(ev)
+
+    _MAX_BACKUP_RUNS = 64
+
+    def _row_runs(self, idx: torch.Tensor, host_idx: torch.Tensor, pool_rows: int) -> list | None:
+        """The prompt's rows as runs (pool row, host row, length) consecutive on both sides, for
+        copy-engine copies; None (the copy kernel) past _MAX_BACKUP_RUNS runs or for rows
+        outside the buffers.  Reads both index lists on the host (a synchronisation)."""
+        src, dst = idx.cpu(), host_idx.cpu()
+        n = src.numel()
+        if n == 0:
+            return []
+        if int(src.min()) < 0 or int(src.max()) >= pool_rows or int(dst.min()) < 0 \
+                or int(dst.max()) >= self.host_k_all.shape[1]:
+            return None
+        cut = (torch.nonzero((src[1:] != src[:-1] + 1) | (dst[1:] != dst[:-1] + 1)).flatten() + 1).tolist()
+        if len(cut) + 1 > self._MAX_BACKUP_RUNS:
+            return None
+        starts, ends = [0] + cut, cut + [n]
+        return [(int(src[a]), int(dst[a]), e - a) for a, e in zip(starts, ends)]
+
+    def _wait_admissions_of(self, req_pool_indices: torch.Tensor) -> None:
+        """Before a step that reads the host tier of these requests: wait for their pending
+        admission backups (every pending one when the indices live on the device)."""
+        if req_pool_indices.device.type == "cpu":
+            reqs = [r for r in req_pool_indices.tolist() if r in self._adm_pending]
+        else:
+            reqs = list(self._adm_pending)
+        if reqs and torch.cuda.is_current_stream_capturing():
+            raise RuntimeError(
+                "an admission backup of this batch is still pending: call wait_admission() and run the "
+                "stream past it before capturing a decode step"
+            )
+        for r in reqs:
+            self.wait_admission(r)
+
     def admit_request(
         self,
         req_pool_idx: int,
@@ -224,17 +288,40 @@ class HiSparseCoordinator:
         n = int(prefill_len)
         buf = self.device_buffer_size
         stream = _lib.stream(self.device)
+        self.wait_admission(req)  # the slot's previous backup, if it is still running
         idx = prefill_indices.to(device=self.device, dtype=torch.int64).contiguous()
         host_idx = self.host_allocator.alloc(n)
         pool = token_to_kv_pool
         _lib.call("qq_hisparse_request_state", _lib.ptr(self.buffer_tokens), _lib.ptr(self.lru_slots),
                   self.num_layers, self.max_reqs, buf, _lib.ptr(self.req_to_host_pool),
                   self.max_context_len, req, _lib.ptr(host_idx), n, 0, stream)
-        for src_all, host_base in ((pool.k_all, self._host_k_dev), (pool.v_all, self._host_v_dev)):
-            _lib.call("qq_copy_rows", _lib.ptr(src_all), src_all.stride(0) * src_all.element_size(),
-                      src_all.shape[1], _lib.ptr(idx), host_base,
-                      self.host_k_all.stride(0) * self.host_k_all.element_size(), self.host_k_all.shape[1],
-                      _lib.ptr(host_idx), n, self.num_layers, self.row_bytes, stream)
+        backup_stream = stream
+        runs = None
+        if self.async_admission:
+            side = self._adm_stream
+            side.wait_stream(torch.cuda.current_stream(self.device))  # prompt rows and host rows ready
+            idx.record_stream(side)
+            host_idx.record_stream(side)
+            backup_stream = side.cuda_stream
+            runs = self._row_runs(idx, host_idx, pool.k_all.shape[1])
+        if runs is not None:
+            # the copy engines: decode steps' swap-in kernels on the other stream keep their
+            # host -> device rate while this device -> host backup runs
+            with torch.cuda.stream(self._adm_stream):
+                for s0, h0, m in runs:
+                    for layer in range(self.num_layers):
+                        self.host_k_all[layer, h0 : h0 + m].copy_(pool.k_all[layer, s0 : s0 + m], non_blocking=True)
+                        self.host_v_all[layer, h0 : h0 + m].copy_(pool.v_all[layer, s0 : s0 + m], non_blocking=True)
+        else:
+            for src_all, host_base in ((pool.k_all, self._host_k_dev), (pool.v_all, self._host_v_dev)):
+                _lib.call("qq_copy_rows", _lib.ptr(src_all), src_all.stride(0) * src_all.element_size(),
+                          src_all.shape[1], _lib.ptr(idx), host_base,
+                          self.host_k_all.stride(0) * self.host_k_all.element_size(), self.host_k_all.shape[1],
+                          _lib.ptr(host_idx), n, self.num_layers, self.row_bytes, backup_stream)
+        if self.async_admission:
+            ev = torch.cuda.Event()
+            ev.record(self._adm_stream)
+            self._adm_pending[req] = ev
         n_dev = min(n, buf)
         dev_rows = self.req_to_device_buffer[req, :n_dev].contiguous()
         for src_all, dst_all in ((pool.k_all, self.device_k_all), (pool.v_all, self.device_v_all)):
@@ -262,6 +349,8 @@ class HiSparseCoordinator:
             return
         if bs > self.max_reqs:
             raise ValueError(f"batch {bs} exceeds max_reqs {self.max_reqs}")
+        if self._adm_pending:
+            self._wait_admissions_of(req_pool_indices)
         stream = _lib.stream(self.device)
         rpi = req_pool_indices.to(device=self.device, dtype=torch.int64).contiguous()
         seq = seq_lens.to(device=self.device, dtype=torch.int64).contiguous()
@@ -312,6 +401,8 @@ class HiSparseCoordinator:
         bs = int(req_pool_indices.shape[0])
         if bs > self.max_reqs:
             raise ValueError(f"batch {bs} exceeds max_reqs {self.max_reqs}")
+        if self._adm_pending:
+            self._wait_admissions_of(req_pool_indices)
         rpi = req_pool_indices.to(device=self.device, dtype=torch.int64).contiguous()
         seq = seq_lens.to(device=self.device, dtype=torch.int64).contiguous()
         pos = top_k_result.to(device=self.device, dtype=torch.int32)
@@ -381,6 +472,7 @@ class HiSparseCoordinator:
     def request_finished(self, req_pool_idx: int) -> None:
         """[H4] Free the host rows, reset the request's state and bounds (coordinator.py:308-316)."""
         req = int(req_pool_idx)
+        self.wait_admission(req)  # its host rows are not freed under a running backup
         self.host_allocator.free(self.req_to_host_pool[req])  # its rows >= 0, in position order
         _lib.call("qq_hisparse_request_state", _lib.ptr(self.buffer_tokens), _lib.ptr(self.lru_slots),
                   self.num_layers, self.max_reqs, self.device_buffer_size, _lib.ptr(self.req_to_host_pool),

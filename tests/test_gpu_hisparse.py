@@ -18,7 +18,8 @@ DEV = torch.device("cuda", 0)
 LAYERS, KV, D = 2, 2, 8
 
 
-def make(buf: int, top_k: int, page: int = 1, max_reqs: int = 2, max_ctx: int = 256, dtype=torch.float32):
+def make(buf: int, top_k: int, page: int = 1, max_reqs: int = 2, max_ctx: int = 256, dtype=torch.float32,
+         async_admission: bool = False):
     from qwenquest_amd.hisparse import HiSparseCoordinator
     from qwenquest_amd.memory import MHATokenToKVPool
     from qwenquest_amd.quest import QuestAlgorithm
@@ -28,7 +29,7 @@ def make(buf: int, top_k: int, page: int = 1, max_reqs: int = 2, max_ctx: int = 
     coord = HiSparseCoordinator(
         quest=quest, num_layers=LAYERS, kv_heads=KV, head_dim=D, max_reqs=max_reqs,
         max_context_len=max_ctx, top_k=top_k, device_buffer_size=buf,
-        host_pool_size=max_reqs * max_ctx, dtype=dtype, device=DEV,
+        host_pool_size=max_reqs * max_ctx, dtype=dtype, device=DEV, async_admission=async_admission,
     )
     pool = MHATokenToKVPool(max_ctx, LAYERS, KV, D, dtype, DEV)
     return quest, coord, pool
@@ -262,8 +263,9 @@ def test_quest_hisparse_is_bit_identical_to_quest(avoid, shape):
     """reference tests/test_engine.py:59-69 and test_bf16.py:27-43 at the backend boundary:
     the same q/k/v through QuestOnlyBackend and QuestHiSparseBackend over many decode steps
     (the hot buffer must swap) give bit-identical outputs and positions, also where quest
-    runs the fused layer step; QuestHiSparseBackend with swap_route="memcpy" gives the same
-    bits and the same hot-buffer state as with the in-kernel copy."""
+    runs the fused layer step; QuestHiSparseBackend with swap_route="memcpy", or with the
+    admission backup on a side stream (async_admission), gives the same bits, the same
+    hot-buffer state and the same host tier as with the in-kernel copy."""
     from qwenquest_amd.attention.quest_hisparse import QuestHiSparseBackend
     from qwenquest_amd.attention.quest_only import QuestOnlyBackend
     from qwenquest_amd.batch import ForwardBatch, ForwardMode
@@ -279,14 +281,15 @@ def test_quest_hisparse_is_bit_identical_to_quest(avoid, shape):
     vv = torch.randn(L, 2, total, KVH, DIM, generator=gen).to(torch.bfloat16)
     qq = torch.randn(steps, L, 2, H, DIM, generator=gen).to(torch.bfloat16)
     outs, poss, stats = {}, {}, {}
-    for mode in ("quest", "quest_hisparse", "quest_hisparse_memcpy"):
+    for mode in ("quest", "quest_hisparse", "quest_hisparse_memcpy", "quest_hisparse_async"):
         rtp = ReqToTokenPool(2, CTX, DEV)
         kvp = MHATokenToKVPool(2 * CTX, L, KVH, DIM, torch.bfloat16, DEV)
         if mode == "quest":
             be = QuestOnlyBackend(rtp, kvp, cfg)
         else:
             be = QuestHiSparseBackend(rtp, kvp, cfg, host_pool_size=2 * CTX,
-                                      swap_route="memcpy" if mode.endswith("memcpy") else "kernel")
+                                      swap_route="memcpy" if mode.endswith("memcpy") else "kernel",
+                                      async_admission=mode.endswith("async"))
         for r, n in prompts.items():
             rtp.req_to_token[r] = torch.arange(1 + r * CTX, 1 + (r + 1) * CTX, dtype=torch.int32)
             rows = torch.arange(1 + r * CTX, 1 + r * CTX + n)
@@ -319,7 +322,9 @@ def test_quest_hisparse_is_bit_identical_to_quest(avoid, shape):
         if mode != "quest":
             st = be.coord.stats
             assert st.misses > 0 and st.hits > 0
-            stats[mode] = (st, be.coord.buffer_tokens.cpu(), be.coord.lru_slots.cpu(), be.coord.device_k_all.cpu())
+            stats[mode] = (st, be.coord.buffer_tokens.cpu(), be.coord.lru_slots.cpu(), be.coord.device_k_all.cpu(),
+                           be.coord.host_k_all.clone(), be.coord.host_v_all.clone())
+            assert be.coord.admission_done(0) and be.coord.admission_done(1)
     fused = _lib.load().qq_quest_fused_step(_lib.DTYPE_BF16, _lib.DTYPE_BF16, _lib.DTYPE_BF16, H, KVH, DIM, P, TOP_K,
                                             (CTX + P - 1) // P)
     assert fused == (shape == len(BIT_IDENTITY) - 1)
@@ -329,8 +334,66 @@ def test_quest_hisparse_is_bit_identical_to_quest(avoid, shape):
     # stream, scatter) leaves the same hot buffers and gives the same bits
     assert torch.equal(poss["quest_hisparse_memcpy"], poss["quest_hisparse"])
     assert torch.equal(outs["quest_hisparse_memcpy"], outs["quest_hisparse"])
-    a, b = stats["quest_hisparse"], stats["quest_hisparse_memcpy"]
-    assert a[0] == b[0] and all(torch.equal(x, y) for x, y in zip(a[1:], b[1:]))
+    for other in ("quest_hisparse_memcpy", "quest_hisparse_async"):
+        a, b = stats["quest_hisparse"], stats[other]
+        assert a[0] == b[0] and all(torch.equal(x, y) for x, y in zip(a[1:], b[1:])), other
+    assert torch.equal(poss["quest_hisparse_async"], poss["quest_hisparse"])
+    assert torch.equal(outs["quest_hisparse_async"], outs["quest_hisparse"])
+
+
+def test_async_admission_waits_only_for_the_batch_members():
+    """The admission backup on a side stream: pending per request until a decode step of a
+    batch holding that request (host indices: only its members wait; device indices: every
+    pending one), its release or an explicit wait; the host tier ends as a synchronous
+    admission leaves it.  Requests 0 and 2 have their prompts in consecutive pool rows (the
+    copy-engine backup), request 1 in scattered rows (more runs than the copy engines take:
+    the copy kernel on the side stream)."""
+    from qwenquest_amd.memory import MHATokenToKVPool
+
+    CTX = 256
+    prompts = {0: 120, 1: 90, 2: 60}
+    truths = {r: truth(n, seed=10 + r) for r, n in prompts.items()}
+    coords = {}
+    for mode in (False, True):
+        _, coord, _ = make(buf=16, top_k=8, max_reqs=3, max_ctx=CTX, async_admission=mode)
+        pool = MHATokenToKVPool(3 * CTX, LAYERS, KV, D, torch.float32, DEV)
+        for r, n in prompts.items():  # each prompt in rows of its own
+            order = torch.randperm(n, generator=torch.Generator().manual_seed(r)) if r == 1 else torch.arange(n)
+            locs = (1 + r * CTX + order).to(DEV)
+            k, v = truths[r]
+            for layer in range(LAYERS):
+                pool.set_kv_buffer(layer, locs, k[layer].to(DEV), v[layer].to(DEV))
+            coord.admit_request(r, n, pool, locs)
+        coords[mode] = coord
+    coord = coords[True]
+    assert sorted(coord._adm_pending) == [0, 1, 2]
+    locs1 = (1 + CTX + torch.randperm(90, generator=torch.Generator().manual_seed(1))).to(DEV)
+    assert coord._row_runs(locs1, torch.arange(90, device=DEV), 3 * CTX + 1) is None
+    assert coord._row_runs(torch.arange(5, 9, device=DEV), torch.arange(40, 44, device=DEV), 3 * CTX + 1) == [(5, 40, 4)]
+    steps = [(torch.tensor([1]), torch.tensor([91])), ("release", 2),
+             (torch.tensor([0, 1], device=DEV), torch.tensor([121, 92], device=DEV))]
+    pending_after = [[0, 2], [0], []]
+    for c in (coords[False], coord):
+        for (what, arg), left in zip(steps, pending_after):
+            if isinstance(what, str):
+                c.request_finished(arg)
+            else:
+                c.prepare_decode_step(what, arg)
+            if c is coord:
+                assert sorted(c._adm_pending) == left
+    torch.cuda.synchronize()
+    assert all(coord.admission_done(r) for r in range(3))
+    ref = coords[False]
+    assert torch.equal(ref.req_to_host_pool.cpu(), coord.req_to_host_pool.cpu())
+    rows = ref.req_to_host_pool[:2].flatten()
+    rows = rows[rows >= 0].cpu()
+    assert rows.numel() >= 120 + 90
+    assert torch.equal(ref.host_k_all[:, rows], coord.host_k_all[:, rows])
+    assert torch.equal(ref.host_v_all[:, rows], coord.host_v_all[:, rows])
+    for r, n in ((0, 120), (1, 90)):  # the prompts themselves
+        hr = coord.req_to_host_pool[r, :n].cpu()
+        assert torch.equal(coord.host_k_all[:, hr], truths[r][0])
+        assert torch.equal(coord.host_v_all[:, hr], truths[r][1])
 
 
 def test_device_row_allocator_hands_out_rows_in_the_reference_order():
