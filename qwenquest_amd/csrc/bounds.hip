@@ -71,7 +71,7 @@ __device__ inline int64_t load_index(const void* p, int is64, int64_t i) {
 // rows with independent loads (one row = KV*D contiguous elements, so each
 // row step of the block is one coalesced KV*D-element read).
 constexpr int kRowChunk = 256;
-constexpr int kWaveFoldBatch = 16;  // rows in flight per wave of prefill_bounds_wave_kernel
+constexpr int kWaveFoldBatch = 32;  // rows in flight per wave of prefill_bounds_wave_kernel
 constexpr int kWavePages = 1;      // pages per wave of prefill_bounds_wave_kernel
 
 __global__ __launch_bounds__(kThreads) void prefill_bounds_kernel(PrefillArgs a) {
