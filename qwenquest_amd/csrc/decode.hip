@@ -628,7 +628,10 @@ __global__ __launch_bounds__(64 * W, 8 / W) void quest_attend_unit_kernel(StepAr
     for (int t = 0; t < 4; ++t)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const uint16_t pbits = f2bf(exp2f(acc[t][i] - Mn));
+        // v_exp_f32 as it is (exp2f adds a rescale for results below 2^-126, which only
+        // the weights of rows 126 binary orders under the maximum reach) and the hardware's
+        // round-to-nearest-even bf16 conversion, equal to f2bf for every value that is not NaN
+        const uint16_t pbits = __builtin_bit_cast(uint16_t, (__bf16)__builtin_amdgcn_exp2f(acc[t][i] - Mn));
         sum += bf2f(pbits);
         pa[t][i] = (short)pbits;
       }
