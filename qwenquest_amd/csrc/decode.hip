@@ -759,13 +759,30 @@ static bool fused_shape(int q_dtype, int kv_dtype, int new_dtype, int num_q_head
          max_pages <= 24 * 64 * kUnitMinWaves;
 }
 
-// Waves per block of the unit attention: 8 (one block per CU) when the batch has
-// a 64-slot unit for every wave of one 8-wave block per CU, else 4 (two per CU).
-static int unit_waves(int bs, int top_k) {
-  return (int64_t)bs * kStepKV * (top_k / 64) >= 8LL * device_cu_count() ? 8 : 4;
+// Launch shape of the unit attention: W waves per block, `parts` blocks per (request,
+// KV head); a wave takes the units p*W + w, p*W + w + W*parts, ... one after the other.
+// The grid is sized to one round of resident blocks, since each block pays its own
+// selection, row lookups and merge before and after its streaming:
+//  * fewer units than one 8-wave block per CU could take: 4-wave blocks, one unit per
+//    wave (as many parts as that needs, up to kUnitParts);
+//  * up to one (request, KV head) pair per CU: 8-wave blocks (one per CU), parts =
+//    CUs / pairs (batch 16 x 2048 slots: 4 parts, one unit per wave; batch 32: 2 parts);
+//  * more pairs: 4-wave blocks (two per CU), parts = ceil(2 CUs / pairs) (1 from 2 pairs
+//    per CU on).
+// Measured at 48 layers: batch 32 x 64K 51.3 -> 45.2 us per layer-step, batch 64 x 32K
+// 83.5 -> 67.1, batch 96 x 21.8K 101.4 -> 93.0, batch 128 x 16K 147.6 -> 111.0 against
+// one unit per wave throughout.
+struct UnitShape {
+  int W, parts;
+};
+static UnitShape unit_shape(int bs, int top_k) {
+  const int64_t c = device_cu_count(), units = top_k / 64, pairs = (int64_t)bs * kStepKV;
+  const int cap8 = std::max(1, std::min(kUnitParts, ceil_div(units, 8)));
+  const int cap4 = std::max(1, std::min(kUnitParts, ceil_div(units, 4)));
+  if (pairs * units < 8 * c) return {4, cap4};
+  if (pairs <= c) return {8, (int)std::max<int64_t>(1, std::min<int64_t>(cap8, c / pairs))};
+  return {4, std::max(1, std::min(cap4, ceil_div(2 * c, pairs)))};
 }
-// Blocks per (request, KV head): one unit per wave where the parts allow it.
-static int step_parts(int top_k, int waves) { return max(1, min(kUnitParts, ceil_div(top_k / 64, waves))); }
 
 extern "C" int qq_quest_fused_step(int q_dtype, int kv_dtype, int new_dtype, int num_q_heads, int kv_heads,
                                    int head_dim, int page_size, int top_k, int max_pages) {
@@ -785,8 +802,8 @@ int qq::attend_rows_fused(const void* q, int64_t q_bstride, int num_q_heads, con
     return 1;
   const int top_k = (int)slots;
   const int G = num_q_heads / kStepKV;
-  const int W = unit_waves(bs, top_k);
-  const int parts = step_parts(top_k, W);
+  const UnitShape us = unit_shape(bs, top_k);
+  const int W = us.W, parts = us.parts;
   const int64_t part_bytes = (int64_t)bs * kStepKV * parts * G * (kMfmaDim + 2) * (int64_t)sizeof(float);
   if (parts > 1 && workspace_bytes < part_bytes) return 1;
   StepArgs a{};
@@ -950,8 +967,8 @@ static int forward_decode(
   sa.pool_rows = kv_rows;
 
   const int G = num_q_heads / kv_heads;
-  const int W = unit_waves(bs, top_k);
-  const int parts = step_parts(top_k, W);
+  const UnitShape us = unit_shape(bs, top_k);
+  const int W = us.W, parts = us.parts;
   const int64_t part_bytes = (int64_t)bs * kv_heads * parts * G * (kMfmaDim + 2) * (int64_t)sizeof(float);
   const bool fused = sync && sync_bytes >= qq_quest_layer_step_sync_bytes(bs, kv_heads) &&
                      fused_shape(q_dtype, kv_dtype, k_new ? new_dtype : -1, num_q_heads, kv_heads, head_dim,

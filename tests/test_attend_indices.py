@@ -38,12 +38,16 @@ def ceil_div(a, b):
     return -(-a // b)
 
 
-def unit_waves(bs, top_k, cus=CUS):
-    return 8 if bs * KV * (top_k // UNIT) >= 8 * cus else 4
-
-
-def step_parts(top_k, waves):
-    return max(1, min(PARTS_MAX, ceil_div(top_k // UNIT, waves)))
+def unit_shape(bs, top_k, cus=CUS):
+    """(waves per block, parts per (request, KV head)) as decode.hip's unit_shape picks them."""
+    units, pairs = top_k // UNIT, bs * KV
+    cap8 = max(1, min(PARTS_MAX, ceil_div(units, 8)))
+    cap4 = max(1, min(PARTS_MAX, ceil_div(units, 4)))
+    if pairs * units < 8 * cus:
+        return 4, cap4
+    if pairs <= cus:
+        return 8, max(1, min(cap8, cus // pairs))
+    return 4, max(1, min(cap4, ceil_div(2 * cus, pairs)))
 
 
 def dense_parts(max_rows):
@@ -119,8 +123,7 @@ def check_launch(top_k, n, parts, per_wave, waves, step_rows, rowcap):
 
 def check_units(top_k, n, bs):
     """The unit kernel's slot coverage for one request of a batch of bs."""
-    waves = unit_waves(bs, top_k)
-    parts = step_parts(top_k, waves)
+    waves, parts = unit_shape(bs, top_k)
     units = top_k // UNIT
     seen = []
     for part in range(parts):
@@ -161,7 +164,7 @@ SEQS = (1, 2, 15, 16, 31, 33, 63, 64, 65, 127, 2047, 2048, 2049, 4095, 4096, 409
 
 
 @pytest.mark.parametrize("top_k", TOPKS)
-@pytest.mark.parametrize("bs", (1, 4, 16, 64))
+@pytest.mark.parametrize("bs", (1, 4, 16, 32, 48, 64, 96, 128, 256))
 def test_unit_attention_slots(top_k, bs):
     for s in SEQS:
         check_units(top_k, min(max(s, 0), top_k), bs)
@@ -172,7 +175,19 @@ def test_benchmark_shape_runs_one_unit_per_wave():
     (one per CU), each wave one 64-row unit."""
     waves, parts = check_units(2048, 2048, 16)
     assert (waves, parts) == (8, 4) and 16 * KV * parts == CUS
-    assert unit_waves(8, 2048) == 4 and step_parts(2048, 4) == 8
+    assert unit_shape(8, 2048) == (4, 8)
+
+
+def test_larger_batches_fill_one_round_of_blocks():
+    """Past batch 16 (2048 slots) a wave takes several units one after the other so that
+    the grid is about one round of resident blocks: 8-wave blocks up to one (request, KV
+    head) pair per CU, then two 4-wave blocks per CU."""
+    for bs, shape, units_per_wave in ((32, (8, 2), 2), (48, (8, 1), 4), (64, (8, 1), 4), (96, (4, 2), 4),
+                                      (128, (4, 1), 8), (256, (4, 1), 8)):
+        waves, parts = check_units(2048, 2048, bs)
+        assert (waves, parts) == shape
+        assert ceil_div(2048 // UNIT, waves * parts) == units_per_wave
+        assert bs * KV * parts <= 4 * CUS
 
 
 @pytest.mark.parametrize("top_k", TOPKS)
@@ -214,9 +229,9 @@ def test_dense_attention_geometry(max_rows):
         check_launch(max_rows, n, parts, per_wave, HEAD_WAVES, 32, HEAD_ROWCAP)
 
 
-@pytest.mark.parametrize("bs,top_k,G", list(itertools.product((1, 3, 16, 64), (64, 2048, 4096), (1, 8, 16))))
+@pytest.mark.parametrize("bs,top_k,G", list(itertools.product((1, 3, 16, 64, 128), (64, 2048, 4096), (1, 8, 16))))
 def test_partials_and_counters_in_bounds(bs, top_k, G):
-    parts = step_parts(top_k, unit_waves(bs, top_k))
+    parts = unit_shape(bs, top_k)[1]
     assert parts <= PARTS_MAX  # one merge pass
     ws_floats = bs * KV * parts * G * (128 + 2)
     o_floats = bs * KV * parts * G * 128

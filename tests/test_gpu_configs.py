@@ -346,13 +346,16 @@ def test_contexts_past_the_fused_selection_400k():
                 assert_attn_close(outs[step, i].float().numpy(), ref, f"step {step} request {i}")
 
 
-def test_batch64_one_part_per_head():
-    """Batch 64 x 8192 tokens: with 64 x 4 (request, KV head) pairs on the CUs the fused
-    attention runs one part per head (no partial merge, 2048 rows per block); positions
-    bit-exact vs the oracle, attention within attn_tol, over 3 decode steps."""
+@pytest.mark.parametrize("B", [32, 64, 96, 128])
+def test_larger_batches_units_one_after_another(B):
+    """Batches past 16 requests: the fused attention's grid is one round of resident blocks
+    (batch 32: 8-wave blocks, 2 parts per (request, KV head); 64: one part, 4 units per wave
+    one after another, no partial merge; 96: 4-wave blocks, 2 parts; 128: 4-wave blocks, one
+    part, 8 units per wave); positions bit-exact vs the oracle on every request, attention
+    within attn_tol on every 7th, over 3 decode steps."""
     from qwenquest_amd.batch import ForwardBatch, ForwardMode
 
-    B, S, steps = 64, 8192, 3
+    S, steps = (8192 if B <= 64 else 4096), 3
     ctx = S + steps + 64
     rtp, kvp, be, base = make_quest_backend(B, ctx, 1)
     kvp.k_all[0].copy_(dev_randn((B * ctx + 1, KV, D), 31).to(torch.bfloat16))
@@ -390,6 +393,49 @@ def test_batch64_one_part_per_head():
             ref = oracle_attention(qc[i], kk[rows], vv[rows])
             assert_attn_close(out[i], ref, f"step {step} request {i}")
         assert np.array_equal(pos[:, :TOP_K], ref_pos[:, :TOP_K])
+
+
+def test_batch128_quest_and_hisparse_bit_identical():
+    """Batch 128 x 8192 tokens (4-wave blocks, one part per (request, KV head), 8 units per
+    wave): QuestOnlyBackend and QuestHiSparseBackend (whose attention over its hot-buffer
+    rows takes the same launch shape) give the same positions and output bits over 4
+    decode steps, with misses in the hot buffer."""
+    from qwenquest_amd.batch import ForwardBatch, ForwardMode
+
+    B, S, steps = 128, 8192, 4
+    ctx = S + steps + 64
+    k = dev_randn((B * ctx + 1, KV, D), 41).to(torch.bfloat16)
+    v = dev_randn((B * ctx + 1, KV, D), 42).to(torch.bfloat16)
+    qs = dev_randn((steps, B, H, D), 43).to(torch.bfloat16)
+    prompt = S - 1
+    results = {}
+    for mode in ("quest", "quest_hisparse"):
+        rtp, kvp, be, base = make_quest_backend(B, ctx, 1, hisparse=mode == "quest_hisparse")
+        kvp.k_all[0].copy_(k)
+        kvp.v_all[0].copy_(v)
+        pre = ForwardBatch(ForwardMode.EXTEND, None, None, torch.arange(B), torch.full((B,), prompt), None,
+                           rtp, kvp, be)
+        if mode == "quest":
+            be._update_quest_for_extend(pre)
+        else:
+            be.on_extend_finished(pre)
+        outs, poss = [], []
+        for step in range(steps):
+            seq = torch.full((B,), S + step, device=DEV, dtype=torch.int64)
+            loc = base + seq - 1
+            batch = ForwardBatch(ForwardMode.DECODE, None, None, torch.arange(B, device=DEV), seq,
+                                 loc if mode == "quest" else None, rtp, kvp, be)
+            be.init_forward_metadata(batch)
+            out = be.forward_decode(qs[step], k[loc], v[loc], Layer(0), batch)
+            outs.append(out.cpu())
+            poss.append(be._positions[:B].cpu())
+        results[mode] = (torch.stack(outs), torch.stack(poss))
+        if mode == "quest_hisparse":
+            assert be.coord.stats.misses > 0
+        del rtp, kvp, be
+        torch.cuda.empty_cache()
+    assert torch.equal(results["quest"][1], results["quest_hisparse"][1])
+    assert torch.equal(results["quest"][0], results["quest_hisparse"][0])
 
 
 def test_c4_hisparse_batch16_128k_ar1_queries():
