@@ -73,6 +73,7 @@ __device__ inline int64_t load_index(const void* p, int is64, int64_t i) {
 constexpr int kRowChunk = 256;
 constexpr int kWaveFoldBatch = 32;  // rows in flight per wave of prefill_bounds_wave_kernel
 constexpr int kWavePages = 1;      // pages per wave of prefill_bounds_wave_kernel
+constexpr int kPfThreads = 128;  // 2 waves per block of prefill_bounds_wave_kernel
 
 __global__ __launch_bounds__(kThreads) void prefill_bounds_kernel(PrefillArgs a) {
   const int64_t page = blockIdx.x;
@@ -274,10 +275,10 @@ __device__ inline uint32_t bf16x2_special(uint32_t w) {
 // torch.minimum / maximum semantics.  A row outside the buffer is not folded (its load
 // reads row 0).
 template <int B, int PPW>
-__global__ __launch_bounds__(kThreads) void prefill_bounds_wave_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(kPfThreads) void prefill_bounds_wave_kernel(PrefillArgs a) {
   constexpr int C = 512;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int64_t page0 = ((int64_t)blockIdx.x * (kThreads / 64) + wave) * PPW;
+  const int64_t page0 = ((int64_t)blockIdx.x * (kPfThreads / 64) + wave) * PPW;
   const int li = blockIdx.y;
   const int layer = a.layer_begin + li;
   if (a.set_counters && page0 == 0 && li == a.n_layers - 1 && lane == 0) {
@@ -605,7 +606,7 @@ extern "C" int qq_quest_prefill_bounds(const void* k_base, int64_t k_layer_strid
     prefill_bounds_kernel<<<grid, kThreads, 0, s>>>(a);
   else if (C == 512 && k_rows <= INT32_MAX)
     prefill_bounds_wave_kernel<kWaveFoldBatch, kWavePages>
-        <<<dim3(ceil_div(pages, kThreads / 64 * kWavePages), n_layers), kThreads, 0, s>>>(a);
+        <<<dim3(ceil_div(pages, kPfThreads / 64 * kWavePages), n_layers), kPfThreads, 0, s>>>(a);
   else if (C == 512)
     prefill_bounds_wide_kernel<64><<<grid, kThreads, 0, s>>>(a);
   else if (C == 1024)

@@ -1,15 +1,15 @@
 """CPU model of prefill_bounds_wave_kernel's geometry (bounds.hip): the launch covers every
 page of the prompt exactly once, each wave folds its page's rows [begin, end) once each and
-in order (64-row index chunks, batches of 16 loads), and every index it reads lies in
+in order (64-row index chunks, batches of 32 loads), and every index it reads lies in
 [0, n_tokens).  Mirrors the kernel's loops; no GPU."""
 
 from __future__ import annotations
 
 import pytest
 
-WAVES_PER_BLOCK = 4  # 256-thread blocks
+WAVES_PER_BLOCK = 2  # 128-thread blocks
 PAGES_PER_WAVE = 1
-BATCH = 16
+BATCH = 32
 CHUNK = 64
 
 
