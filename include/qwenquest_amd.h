@@ -84,6 +84,18 @@ int qq_quest_decode_update(const void* k_base, int64_t k_layer_stride, int k_dty
                            int num_layers, int max_reqs, int max_pages, int kv_heads,
                            int head_dim, int page_size, void* stream);
 
+/* Replaces the row lookup of QuestOnlyBackend._do_quest_decode_step_update
+ * (src/qwenquest/attention/quest_only.py:84-97): for batch entry i, request
+ * r = req_pool_indices[i], the previous step's token sits at position
+ * p = max(seq_lens[i] - 2, 0); device_locs_out[i] = req_to_token[r, p], or -1 when
+ * the request is on its first decode step after prefill (skip_first[r] != 0) or r
+ * or p lies outside the table.  skip_first[r] is then cleared for every listed
+ * request (after all lookups, so a request listed twice reads the flag once as
+ * set).  The result feeds qq_quest_decode_update. */
+int qq_quest_decode_step_locs(const int64_t* req_pool_indices, const int64_t* seq_lens, int bs,
+                              uint8_t* skip_first, const int32_t* req_to_token, int64_t r2t_rows,
+                              int64_t r2t_stride, int64_t* device_locs_out, void* stream);
+
 /* Replaces QuestAlgorithm.maybe_finalize_decode_representations
  * (src/qwenquest/quest.py:304-321): for requests whose running_token_count is
  * P-1, copy the running bounds into page running_page_idx (all layers), reset

@@ -62,6 +62,7 @@ class QuestOnlyBackend(AttentionBackend):
             head_dim=token_to_kv_pool.head_dim,
         )
         self._skip_first_decode_update = torch.zeros(req_to_token_pool.size, dtype=torch.bool, device=device)
+        self._step_locs = torch.empty(req_to_token_pool.size, dtype=torch.int64, device=device)
         self._positions = torch.empty((req_to_token_pool.size, cfg.top_k), dtype=torch.int32, device=device)
         self._attn_ws = AttentionWorkspace(device)
         # counters of the fused (two-launch) layer step: zeroed once, left zeroed by every
@@ -80,16 +81,20 @@ class QuestOnlyBackend(AttentionBackend):
         """[Q3] The previous step's token sits at position ``seq_len - 2`` (quest_only.py:84-97).
 
         Requests on their first decode step after prefill get row -1, which the
-        fused kernel skips (no fold, no counter advance), without a host sync.
+        fused kernel skips (no fold, no counter advance), without a host sync: one
+        kernel looks the rows up and clears the first-step flags.
         """
         dev = self.quest.device
-        rpi = req_pool_indices.to(device=dev, dtype=torch.int64)
-        seq = seq_lens.to(device=dev, dtype=torch.int64)
-        skip = self._skip_first_decode_update[rpi]
-        self._skip_first_decode_update.index_fill_(0, rpi, False)  # no host copy: graph-capturable
-        prev = (seq - 2).clamp(min=0)
-        locs = self.req_to_token[rpi, prev].to(torch.int64)
-        locs = torch.where(skip, torch.full_like(locs, -1), locs)
+        rpi = req_pool_indices.to(device=dev, dtype=torch.int64).contiguous()
+        seq = seq_lens.to(device=dev, dtype=torch.int64).contiguous()
+        bs = int(rpi.numel())
+        if bs > self._step_locs.numel():
+            raise ValueError(f"batch {bs} exceeds the request pool ({self._step_locs.numel()})")
+        locs = self._step_locs[:bs]
+        r2t = self.req_to_token
+        _lib.call("qq_quest_decode_step_locs", _lib.ptr(rpi), _lib.ptr(seq), bs,
+                  _lib.ptr(self._skip_first_decode_update), _lib.ptr(r2t), r2t.shape[0], r2t.stride(0),
+                  _lib.ptr(locs), _lib.stream(dev))
         self.quest.update_decode_representations_fused(rpi, self.token_to_kv_pool.k_all, locs)
 
     # ----------------------------------------------------------------- prefill
