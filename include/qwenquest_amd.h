@@ -321,7 +321,11 @@ int qq_kv_scatter(void* k_layer, void* v_layer, int buf_dtype, int64_t kv_rows, 
  * are all -1 (the rows attention then outputs NaN for it).  error_mirror (a
  * device-accessible pointer to 3 int32 in pinned host memory, or NULL) gets
  * word 0 / word 1 set to 1 with the same conditions, so the host can poll for
- * errors without a device synchronisation. */
+ * errors without a device synchronisation.  new_k / new_v (both or neither): the
+ * step's new K and V rows ([bs] rows of row_bytes, the hot buffer's dtype), which
+ * the plan also writes into each request's newest slot, row
+ * req * (buf + 1) + min(seq - 1, buf) - HiSparseCoordinator.write_new_token
+ * (coordinator.py:217-228) in the same launch. */
 int qq_hisparse_swap_in(const int32_t* positions, int64_t positions_stride,
                         const int32_t* actual_lens, const int64_t* seq_lens,
                         const int64_t* req_pool_indices, int bs, int max_reqs,
@@ -331,7 +335,8 @@ int qq_hisparse_swap_in(const int32_t* positions, int64_t positions_stride,
                         const void* host_k_layer, const void* host_v_layer, int64_t row_bytes,
                         int64_t host_rows, int64_t* rows_out, int64_t* copy_dst,
                         int64_t* copy_src, int32_t* copy_count, uint64_t* stats,
-                        int32_t* error_flags, int32_t* error_mirror, void* stream);
+                        int32_t* error_flags, int32_t* error_mirror, const void* new_k,
+                        const void* new_v, void* stream);
 
 /* qq_hisparse_swap_in without its copy: the plan only (rows_out, buffer_tokens,
  * lru_slots, stats and errors as there); the layer's misses are left in

@@ -83,7 +83,7 @@ SIGNATURES: dict[str, tuple] = {
     "qq_hisparse_swap_in": (
         _I,
         [_P, _L, _P, _P, _P, _I, _I, _I, _I, _P, _P, _P, _L, _P, _P, _P, _P, _L, _L, _P, _P, _P,
-         _P, _P, _P, _P, _P],
+         _P, _P, _P, _P, _P, _P, _P],
     ),
     "qq_hisparse_swap_plan": (
         _I,

@@ -123,9 +123,15 @@ class QuestHiSparseBackend(AttentionBackend):
     def forward_decode(self, q, k, v, layer, batch: ForwardBatch) -> torch.Tensor:
         """quest_hisparse.py:112-133."""
         reqs, seq_lens = batch.req_pool_indices, batch.seq_lens
-        self.coord.write_new_token(layer.layer_id, reqs, seq_lens, k, v)
+        coord = self.coord
+        # the new token rides with the swap-in launch when it needs no conversion
+        # (the selection does not read the hot buffer, the attention reads it after the swap-in)
+        fused_new = coord.swap_route == "kernel" and k.dtype == coord.dtype and v.dtype == coord.dtype
+        if not fused_new:
+            coord.write_new_token(layer.layer_id, reqs, seq_lens, k, v)
         positions, actual = self.quest.retrieve_topk(q, layer.layer_id, reqs, seq_lens, out=self._positions)
-        rows = self.coord.swap_in_selected_pages(reqs, seq_lens, positions, layer.layer_id, actual_lens=actual)
+        rows = coord.swap_in_selected_pages(reqs, seq_lens, positions, layer.layer_id, actual_lens=actual,
+                                            new_k=k if fused_new else None, new_v=v if fused_new else None)
         bs = batch.batch_size
         q3 = self.quest._queries_3d(q)
         return decode_attention_rows(

@@ -67,6 +67,10 @@ struct SwapArgs {
   const char* host_k;
   const char* host_v;
   int64_t row_bytes, dev_rows, host_rows;
+  // the step's new K / V rows ([bs] rows of row_bytes, the hot buffer's dtype), written to
+  // each request's newest slot by the plan kernel; null: written elsewhere
+  const char* new_k;
+  const char* new_v;
 };
 
 __device__ inline uint32_t slot_hash(int p, int mask) {
@@ -194,6 +198,18 @@ __global__ __launch_bounds__(kPlanThreads) void swap_plan_kernel(SwapArgs a) {
     return;
   }
   const int64_t base_row = req * (int64_t)(buf + 1);
+  if (a.new_k && s >= 1) {  // the new token into its newest slot (coordinator.py:217-228)
+    const int64_t loc = base_row + min(s - 1, (int64_t)buf);
+    const int64_t units = a.row_bytes / 16;
+    if (loc < a.dev_rows) {
+      for (int64_t u = tid; u < 2 * units; u += kPlanThreads) {
+        const bool v = u >= units;
+        const int64_t w = v ? u - units : u;
+        const uint4 x = reinterpret_cast<const uint4*>((v ? a.new_v : a.new_k) + (int64_t)b * a.row_bytes)[w];
+        reinterpret_cast<uint4*>((v ? a.dev_v : a.dev_k) + loc * a.row_bytes)[w] = x;
+      }
+    }
+  }
   if (s <= buf) {  // fast path: the whole sequence is resident, slot == position
     for (int i = tid; i < a.top_k; i += kPlanThreads) rows[i] = i < n ? base_row + pos[i] : -1;
     if (tid == 0) {
@@ -740,7 +756,7 @@ static int swap_in(const char* what, bool copy, const int32_t* positions, int64_
                    void* device_k_layer, void* device_v_layer, const void* host_k_layer, const void* host_v_layer,
                    int64_t row_bytes, int64_t host_rows, int64_t* rows_out, int64_t* copy_dst, int64_t* copy_src,
                    int32_t* copy_count, uint64_t* stats, int32_t* error_flags, int32_t* error_mirror,
-                   void* stream) {
+                   const void* new_k, const void* new_v, void* stream) {
   QQ_REQUIRE(bs >= 0 && max_reqs > 0 && device_buffer_size >= top_k && top_k > 0,
              "%s: bad sizes (buf %d, top_k %d)", what, device_buffer_size, top_k);
   QQ_REQUIRE(device_buffer_size <= kMaxPerThread * kPlanThreads && top_k <= kMaxPerThread * kPlanThreads,
@@ -791,6 +807,8 @@ static int swap_in(const char* what, bool copy, const int32_t* positions, int64_
   a.row_bytes = row_bytes;
   a.dev_rows = (int64_t)max_reqs * (device_buffer_size + 1);
   a.host_rows = host_rows;
+  a.new_k = static_cast<const char*>(new_k);
+  a.new_v = static_cast<const char*>(new_v);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (top_k <= kSmallEntries * kPlanThreads && device_buffer_size <= kSmallSlots * kPlanThreads)
     swap_plan_kernel<kSmallEntries, kSmallSlots><<<bs, kPlanThreads, smem, s>>>(a);
@@ -811,11 +829,13 @@ extern "C" int qq_hisparse_swap_in(const int32_t* positions, int64_t positions_s
                                    const void* host_v_layer, int64_t row_bytes,
                                    int64_t host_rows, int64_t* rows_out, int64_t* copy_dst,
                                    int64_t* copy_src, int32_t* copy_count, uint64_t* stats,
-                                   int32_t* error_flags, int32_t* error_mirror, void* stream) {
+                                   int32_t* error_flags, int32_t* error_mirror, const void* new_k,
+                                   const void* new_v, void* stream) {
+  QQ_REQUIRE((new_k == nullptr) == (new_v == nullptr), "qq_hisparse_swap_in: new_k and new_v go together");
   return swap_in("qq_hisparse_swap_in", true, positions, positions_stride, actual_lens, seq_lens, req_pool_indices,
                  bs, max_reqs, device_buffer_size, top_k, buffer_tokens_layer, lru_slots_layer, req_to_host_pool,
                  max_context_len, device_k_layer, device_v_layer, host_k_layer, host_v_layer, row_bytes, host_rows,
-                 rows_out, copy_dst, copy_src, copy_count, stats, error_flags, error_mirror, stream);
+                 rows_out, copy_dst, copy_src, copy_count, stats, error_flags, error_mirror, new_k, new_v, stream);
 }
 
 extern "C" int qq_hisparse_swap_plan(const int32_t* positions, int64_t positions_stride,
@@ -829,7 +849,7 @@ extern "C" int qq_hisparse_swap_plan(const int32_t* positions, int64_t positions
   return swap_in("qq_hisparse_swap_plan", false, positions, positions_stride, actual_lens, seq_lens,
                  req_pool_indices, bs, max_reqs, device_buffer_size, top_k, buffer_tokens_layer, lru_slots_layer,
                  req_to_host_pool, max_context_len, nullptr, nullptr, nullptr, nullptr, 16, 0, rows_out, copy_dst,
-                 copy_src, copy_count, stats, error_flags, error_mirror, stream);
+                 copy_src, copy_count, stats, error_flags, error_mirror, nullptr, nullptr, stream);
 }
 
 extern "C" int qq_copy_rows(const void* src, int64_t src_layer_stride_bytes, int64_t src_rows,

@@ -394,10 +394,15 @@ class HiSparseCoordinator:
         *,
         actual_lens: torch.Tensor | None = None,
         out: torch.Tensor | None = None,
+        new_k: torch.Tensor | None = None,
+        new_v: torch.Tensor | None = None,
     ) -> torch.Tensor:
         """[H3] Make the selected positions device-resident; ``[bs, top_k]`` int64 rows of
         ``device_k/v[layer_id]``, -1 past each request's ``min(seq_len, top_k)``
-        (coordinator.py:232-304)."""
+        (coordinator.py:232-304).  ``new_k``/``new_v`` (``[bs, kv_heads, head_dim]`` in the
+        hot buffer's dtype, swap_route "kernel" only): the step's new token, written to each
+        request's newest slot by the same launch (what write_new_token does,
+        coordinator.py:217-228)."""
         bs = int(req_pool_indices.shape[0])
         if bs > self.max_reqs:
             raise ValueError(f"batch {bs} exceeds max_reqs {self.max_reqs}")
@@ -405,6 +410,16 @@ class HiSparseCoordinator:
             self._wait_admissions_of(req_pool_indices)
         rpi = req_pool_indices.to(device=self.device, dtype=torch.int64).contiguous()
         seq = seq_lens.to(device=self.device, dtype=torch.int64).contiguous()
+        new_ptrs = (None, None)
+        if new_k is not None or new_v is not None:
+            if self.swap_route != "kernel":
+                raise ValueError("the new token rides with the swap-in only on swap_route='kernel'")
+            nk = new_k.reshape(bs, self.row_elems)
+            nv = new_v.reshape(bs, self.row_elems)
+            if nk.dtype != self.dtype or nv.dtype != self.dtype:
+                raise ValueError(f"new K/V dtype {nk.dtype}/{nv.dtype} != hot buffer dtype {self.dtype}")
+            nk, nv = nk.contiguous(), nv.contiguous()
+            new_ptrs = (_lib.ptr(nk), _lib.ptr(nv))
         pos = top_k_result.to(device=self.device, dtype=torch.int32)
         if pos.shape[1] < self.top_k:
             pos = torch.nn.functional.pad(pos, (0, self.top_k - pos.shape[1]))
@@ -433,7 +448,7 @@ class HiSparseCoordinator:
             self._host_layer(self._host_k_dev, layer_id), self._host_layer(self._host_v_dev, layer_id),
             self.row_bytes, self.host_k_all.shape[1], _lib.ptr(rows), _lib.ptr(self._copy_dst),
             _lib.ptr(self._copy_src), _lib.ptr(self._copy_count), _lib.ptr(self._stats), _lib.ptr(self._err),
-            self._err_host_dev, _lib.stream(self.device),
+            self._err_host_dev, new_ptrs[0], new_ptrs[1], _lib.stream(self.device),
         )
         if self.sync_errors:
             self.check_errors()
