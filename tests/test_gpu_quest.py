@@ -795,3 +795,30 @@ def test_fused_layer_step_graph_replay_eager_and_four_launch_agree():
         assert torch.equal(pe, pg) and torch.equal(oe, og), f"graph replay {i} differs from eager"
         assert torch.equal(pe, pf), f"step {i}: four-launch positions differ"
         assert_attn_close(of.float().cpu().numpy(), oe.float().cpu().numpy(), f"step {i}: four-launch vs fused")
+
+
+def test_decode_step_row_lookup():
+    """qq_quest_decode_step_locs (quest_only.py:84-97): the previous token's pool row
+    req_to_token[r, max(seq - 2, 0)] per listed request, -1 on a request's first decode step
+    (its flag read before any clear, also when the request is listed twice) and for requests
+    or positions outside the table; every listed request's flag is cleared."""
+    from qwenquest_amd import _lib
+
+    R, W = 4, 16
+    r2t = (torch.arange(R * W, dtype=torch.int32) * 7 + 3).view(R, W).to(DEV)
+    skip = torch.tensor([1, 0, 1, 1], dtype=torch.uint8, device=DEV)
+    rpi = torch.tensor([0, 2, 0, 1, 5, -1, 1], dtype=torch.int64, device=DEV)
+    seq = torch.tensor([10, 5, 10, 1, 9, 9, 40], dtype=torch.int64, device=DEV)
+    out = torch.full((rpi.numel(),), 99, dtype=torch.int64, device=DEV)
+    _lib.call("qq_quest_decode_step_locs", _lib.ptr(rpi), _lib.ptr(seq), rpi.numel(), _lib.ptr(skip), _lib.ptr(r2t),
+              R, W, _lib.ptr(out), _lib.stream(DEV))
+    torch.cuda.synchronize()
+    t = r2t.cpu().long()
+    expected = [-1, -1, -1, int(t[1, 0]), -1, -1, -1]  # r 0 and 2 skipped; r 1 at p = 0; r 5, -1 outside; p 38 >= W
+    assert out.cpu().tolist() == expected
+    assert skip.cpu().tolist() == [0, 0, 0, 1]
+    skip.zero_()
+    _lib.call("qq_quest_decode_step_locs", _lib.ptr(rpi[:2]), _lib.ptr(seq[:2]), 2, _lib.ptr(skip), _lib.ptr(r2t),
+              R, W, _lib.ptr(out), _lib.stream(DEV))
+    torch.cuda.synchronize()
+    assert out[:2].cpu().tolist() == [int(t[0, 8]), int(t[2, 3])]
