@@ -87,14 +87,16 @@ int qq_quest_decode_update(const void* k_base, int64_t k_layer_stride, int k_dty
 /* Replaces the row lookup of QuestOnlyBackend._do_quest_decode_step_update
  * (src/qwenquest/attention/quest_only.py:84-97): for batch entry i, request
  * r = req_pool_indices[i], the previous step's token sits at position
- * p = max(seq_lens[i] - 2, 0); device_locs_out[i] = req_to_token[r, p], or -1 when
- * the request is on its first decode step after prefill (skip_first[r] != 0) or r
- * or p lies outside the table.  skip_first[r] is then cleared for every listed
+ * p = max(seq_lens[i] - 2, 0); device_locs_out[i] = req_to_token[r * r2t_stride + p],
+ * or -1 when the request is on its first decode step after prefill (skip_first[r] !=
+ * 0) or r lies outside the table's r2t_rows rows or p outside its r2t_cols columns
+ * (r2t_stride >= r2t_cols: a strided view of a wider table is read only within its
+ * own columns).  skip_first[r] is then cleared for every listed
  * request (after all lookups, so a request listed twice reads the flag once as
  * set).  The result feeds qq_quest_decode_update. */
 int qq_quest_decode_step_locs(const int64_t* req_pool_indices, const int64_t* seq_lens, int bs,
                               uint8_t* skip_first, const int32_t* req_to_token, int64_t r2t_rows,
-                              int64_t r2t_stride, int64_t* device_locs_out, void* stream);
+                              int64_t r2t_cols, int64_t r2t_stride, int64_t* device_locs_out, void* stream);
 
 /* Replaces QuestAlgorithm.maybe_finalize_decode_representations
  * (src/qwenquest/quest.py:304-321): for requests whose running_token_count is
@@ -382,7 +384,10 @@ int qq_hisparse_request_state(int64_t* buffer_tokens, int64_t* lru_slots, int nu
  * host_idx[b] = that row and device_rows[b] = req*(buf+1) + min(seq-2, buf) (the
  * previous token's hot-buffer row); skipped entries get -1 in both.  Fewer free
  * rows than entries (TokenToKVPoolAllocator.alloc's error, memory.py:62-66):
- * bit 4 of *error_flags (and error_mirror word 2), nothing taken. */
+ * bit 4 of *error_flags (and error_mirror word 2), nothing taken: host_idx[b] = -1
+ * and req_to_host_pool unchanged, but device_rows[b] is still written for every
+ * entry that wanted a backup, since the reference folds the previous token into the
+ * bounds (coordinator.py:204-208) before its alloc fails (:210). */
 int qq_hisparse_backup_step(const int64_t* req_pool_indices, const int64_t* seq_lens, int bs,
                             uint8_t* skip_flags, int device_buffer_size, int max_reqs,
                             int64_t* req_to_host_pool, int64_t max_context_len, const int64_t* free_ring,

@@ -71,3 +71,9 @@ class AttentionBackend(ABC):
 
     def on_request_finished(self, req_pool_idx: int) -> None:  # noqa: B027 - optional hook
         """Called by the engine before a request slot is reused."""
+
+    def poll_errors(self) -> None:  # noqa: B027 - optional hook
+        """Raise an error the device detected in a decode step whose kernels have finished,
+        without a synchronisation.  A caller that replays a captured decode step calls it after
+        each replay, since no Python check runs inside a replay.  Backends without
+        device-detected errors have nothing to raise."""

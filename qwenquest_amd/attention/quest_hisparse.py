@@ -142,3 +142,12 @@ class QuestHiSparseBackend(AttentionBackend):
 
     def on_request_finished(self, req_pool_idx: int) -> None:
         self.coord.request_finished(req_pool_idx)
+
+    def poll_errors(self) -> None:
+        """The swap-in's and the eager backup's errors (coordinator.py:278-279, 285-286;
+        memory.py:62-66) from the pinned mirror of the device error word, without a
+        synchronisation: an error surfaces at the first poll after the kernel that detected it
+        has finished (after a synchronisation, at once).  A failed request's attention output
+        is NaN in the step that failed.  Eager decode steps poll at the next step's
+        init_forward_metadata; a caller that replays a captured step polls after each replay."""
+        self.coord.check_errors(sync=False)

@@ -93,7 +93,7 @@ class QuestOnlyBackend(AttentionBackend):
         locs = self._step_locs[:bs]
         r2t = self.req_to_token
         _lib.call("qq_quest_decode_step_locs", _lib.ptr(rpi), _lib.ptr(seq), bs,
-                  _lib.ptr(self._skip_first_decode_update), _lib.ptr(r2t), r2t.shape[0], r2t.stride(0),
+                  _lib.ptr(self._skip_first_decode_update), _lib.ptr(r2t), r2t.shape[0], r2t.shape[1], r2t.stride(0),
                   _lib.ptr(locs), _lib.stream(dev))
         self.quest.update_decode_representations_fused(rpi, self.token_to_kv_pool.k_all, locs)
 

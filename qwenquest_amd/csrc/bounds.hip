@@ -488,14 +488,14 @@ __global__ __launch_bounds__(kThreads) void advance_counters_kernel(const int64_
 // block, so the clears wait for all lookups.
 __global__ __launch_bounds__(kThreads) void decode_step_locs_kernel(const int64_t* rpi, const int64_t* seq, int bs,
                                                                    uint8_t* skip, const int32_t* r2t,
-                                                                   int64_t r2t_rows, int64_t r2t_stride,
-                                                                   int64_t* locs) {
+                                                                   int64_t r2t_rows, int64_t r2t_cols,
+                                                                   int64_t r2t_stride, int64_t* locs) {
   for (int i = threadIdx.x; i < bs; i += kThreads) {
     const int64_t r = rpi[i];
     int64_t loc = -1;
     if (r >= 0 && r < r2t_rows && !skip[r]) {
       const int64_t p = max(seq[i] - 2, (int64_t)0);
-      if (p < r2t_stride) loc = r2t[r * r2t_stride + p];
+      if (p < r2t_cols) loc = r2t[r * r2t_stride + p];
     }
     locs[i] = loc;
   }
@@ -711,11 +711,14 @@ extern "C" int qq_quest_decode_finalize(const int64_t* req_indices, int n, uint1
 
 extern "C" int qq_quest_decode_step_locs(const int64_t* req_pool_indices, const int64_t* seq_lens, int bs,
                                          uint8_t* skip_first, const int32_t* req_to_token, int64_t r2t_rows,
-                                         int64_t r2t_stride, int64_t* device_locs_out, void* stream) {
-  QQ_REQUIRE(bs >= 0 && r2t_rows >= 0 && r2t_stride >= 0, "qq_quest_decode_step_locs: bad arguments");
+                                         int64_t r2t_cols, int64_t r2t_stride, int64_t* device_locs_out,
+                                         void* stream) {
+  QQ_REQUIRE(bs >= 0 && r2t_rows >= 0 && r2t_cols >= 0 && r2t_stride >= r2t_cols,
+             "qq_quest_decode_step_locs: bad arguments (rows %lld, columns %lld, stride %lld)", (long long)r2t_rows,
+             (long long)r2t_cols, (long long)r2t_stride);
   if (bs == 0) return QQ_OK;
   decode_step_locs_kernel<<<1, kThreads, 0, static_cast<hipStream_t>(stream)>>>(
-      req_pool_indices, seq_lens, bs, skip_first, req_to_token, r2t_rows, r2t_stride, device_locs_out);
+      req_pool_indices, seq_lens, bs, skip_first, req_to_token, r2t_rows, r2t_cols, r2t_stride, device_locs_out);
   return check_launch("qq_quest_decode_step_locs");
 }
 

@@ -5,25 +5,29 @@
 // Fused path (bf16, KV*D = 4*128, page 64, at most 64 selected pages, at most
 // 6144 pages per request, top_k <= 4096, and a zeroed sync buffer from the
 // caller): two launches.
-//   1. page scores of every long request (score_pages_fast_kernel, one block
-//      per (request, 32 candidate pages), all CUs) and the new token's K/V
-//      (set_kv_buffer, memory.py:114-120).
-//   2. attention, one 4-wave block per (request, KV head, part of the rows),
-//      up to 8 parts (512 blocks at batch 16, two per CU): the block selects
-//      its request's pages from the scores (filter top-k; every block of a
-//      request computes the same list, so no block waits on another), turns
-//      its share of the list into layout positions and pool rows
-//      (req_to_token, quest_only.py:149-151) in LDS - the KV-head-0 blocks
-//      also write the positions - then each of its 4 waves streams its rows in
-//      steps of 16 with an online softmax (MFMA QK^T and PV) at no more than
-//      128 VGPRs, and the waves combine in LDS.  The parts' (m, l, o) partials
-//      go out with agent-scope stores; the block that completes a (request,
-//      KV head) count merges them into the output.
+//   1. page scores of every long request (score_pages_fast_kernel in select.hip,
+//      one 256-thread block per (request, 32 candidate pages), all resident at
+//      once) and the new token's K/V (set_kv_buffer, memory.py:114-120).
+//   2. attention (quest_attend_unit_kernel): the layout's slots come in units of
+//      64 (a selected page, the recent window, or 64 slots of the dense layout).
+//      One block of W waves per (request, KV head, part); unit_shape sizes the
+//      grid to one round of resident blocks (batch 16 x top_k 2048: 8-wave blocks,
+//      4 parts per (request, KV head), 256 blocks, one unit per wave).  Every
+//      block first selects its request's pages from the scores (select_ranked in
+//      qq_quest_dev.h; the blocks of a request compute the same list, so no block
+//      waits on another).  Each wave then resolves its unit's 64 rows itself
+//      (lane l: slot -> position -> req_to_token; the KV-head-0 blocks store the
+//      positions), issues all 32 16-byte loads of the unit's K and V slices at
+//      once (32 KiB per wave, 216 VGPRs, two waves per SIMD), computes
+//      S^T = K Q^T (v_mfma_f32_16x16x32_bf16), one softmax over the 64 rows folded
+//      into its running (M, L), and P V (v_mfma_f32_16x16x16bf16_1k, V transposed
+//      in registers).  The W waves combine in LDS; the parts' (m, l, o) partials go
+//      out with agent-scope stores, and the block that completes a (request, KV
+//      head) count merges them into the output.
 // The counters return to zero before the launch ends, so the next call (or a
-// graph replay) starts clean.  A CU streams only ~30-40 GB/s of these 256-byte
-// row slices, so the attention grid covers every CU.  quest_hisparse's
-// attention over its hot-buffer rows runs the same blocks, so both backends
-// compute the same partials in the same order.
+// graph replay) starts clean.  quest_hisparse's attention over its hot-buffer
+// rows runs the same kernel (its rows mode), in the same unit order, so both
+// backends compute the same partials in the same order.
 //
 // Other shapes: four launches on one stream, each consuming the previous one's
 // output: score (all CUs) -> select + new-token store (one block per request)
@@ -1126,7 +1130,11 @@ extern "C" int qq_quest_forward_decode_noalloc(
   const char* what = "qq_quest_forward_decode_noalloc";
   QQ_REQUIRE(bs >= 0 && max_pages > 0 && kv_heads > 0 && head_dim > 0 && num_q_heads > 0, "%s: bad sizes", what);
   if (bs == 0) return QQ_OK;
-  const int64_t sync_need = qq_quest_layer_step_sync_bytes(bs, kv_heads);
+  // the hand-off counters are read only by the fused layer step; other shapes take the
+  // four-launch path, which needs none
+  const bool fused = fused_shape(q_dtype, kv_dtype, k_new ? new_dtype : -1, num_q_heads, kv_heads, head_dim,
+                                 page_size, top_k, max_pages);
+  const int64_t sync_need = fused ? qq_quest_layer_step_sync_bytes(bs, kv_heads) : 0;
   const int64_t score_need = (int64_t)bs * max_pages * (int64_t)sizeof(float);
   const int64_t work_need = qq_decode_attention_workspace_bytes(bs, top_k, num_q_heads, head_dim);
   QQ_REQUIRE(sync_need <= kScratchSyncBytes && score_need <= kScratchScoreBytes && work_need <= kScratchWorkBytes,

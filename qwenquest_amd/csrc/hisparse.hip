@@ -614,7 +614,8 @@ __global__ __launch_bounds__(256) void ring_free_kernel(int64_t* ring, int64_t* 
 // its request's skip flag is set (first step after admission); otherwise take the next
 // free host row in batch order, record req_to_host_pool[req, seq - 2] and the device
 // row of the previous token.  host_idx[b] / dev_rows[b] are -1 for skipped entries (the
-// fold and the copies skip them).  Too few free rows: error bit 4, nothing taken.
+// fold and the copies skip them).  Too few free rows: error bit 4, nothing taken
+// (host_idx[b] = -1, so nothing is copied), while dev_rows[b] keeps the fold going.
 __global__ __launch_bounds__(256) void backup_step_kernel(const int64_t* rpi, const int64_t* seq, int bs,
                                                         uint8_t* skip, int buf, int R, int64_t* r2h,
                                                         int64_t r2h_stride, const int64_t* ring, int64_t* state,
@@ -677,14 +678,15 @@ __global__ __launch_bounds__(256) void backup_step_kernel(const int64_t* rpi, co
       tot += s_wave[w];
     }
     if (b < bs) {
+      // the fold takes every entry that wanted a backup, also when the host pool is
+      // exhausted: the reference folds first and only then fails in alloc
+      dev_rows[b] = want ? req * (int64_t)(buf + 1) + min(prev, (int64_t)buf) : -1;
       if (want && !oom) {
         const int64_t h = ring[(head + base + wbase + x - 1) % cap];
         host_idx[b] = h;
         r2h[req * r2h_stride + prev] = h;
-        dev_rows[b] = req * (int64_t)(buf + 1) + min(prev, (int64_t)buf);
       } else {
         host_idx[b] = -1;
-        dev_rows[b] = -1;
       }
     }
     base += tot;

@@ -446,7 +446,8 @@ def test_c4_hisparse_batch16_128k_ar1_queries():
     Every step: QuestOnlyBackend and QuestHiSparseBackend on the same pool and inputs give
     bit-identical positions and outputs, and the swap-in rows, buffer_tokens and lru_slots
     equal oracle/hisparse.py's; positions equal the Quest oracle's on sampled steps (page
-    boundaries crossed at steps 1 and 65)."""
+    boundaries crossed at steps 1 and 65), and quest's attention outputs of requests 0, 7 and 15
+    equal the float64 oracle's within attn_tol at steps 0 and 127 in both layers."""
     from oracle import hisparse as oh
     from qwenquest_amd.attention.quest_hisparse import QuestHiSparseBackend
     from qwenquest_amd.attention.quest_only import QuestOnlyBackend
@@ -534,6 +535,16 @@ def test_c4_hisparse_batch16_128k_ar1_queries():
                 ref_pos, ref_actual, _ = st.retrieve_topk(qb[layer].float().cpu().numpy(), layer, reqs)
                 pq, _ = quest_be.quest.retrieve_topk(qb[layer], layer, torch.arange(B, device=DEV), seq)
                 assert np.array_equal(pq.cpu().numpy(), ref_pos[:, :TOP_K]), f"step {step} layer {layer}: vs oracle"
+                if step in (0, 127):
+                    # the layer step's attention at this shape (the fused two-launch path)
+                    # against the float64 oracle over the oracle's rows, new token included
+                    out_q = outs[quest_be.name][layer].float().cpu().numpy()
+                    for i in (0, 7, 15):
+                        n = int(ref_actual[i])
+                        rows = (base[i] + torch.from_numpy(ref_pos[i, :n].astype(np.int64)).to(DEV))
+                        ref = oracle_attention(qb[layer, i].cpu(), kvp.k_all[layer][rows].cpu(),
+                                               kvp.v_all[layer][rows].cpu())
+                        assert_attn_close(out_q[i], ref, f"step {step} layer {layer} request {i}: attention")
         # the new token's keys join the oracle's copy of the pool (folded at the next step)
         for layer in range(L):
             kbits[layer][loc.cpu().numpy()] = bf16_bits(kn[layer].cpu())

@@ -443,18 +443,35 @@ def _his_coord(buf, top_k, ctx, host_pool, kv=2, d=8, dtype=torch.float32, max_r
 
 def test_host_pool_exhaustion_is_raised_from_the_device():
     """The eager backup takes its host rows on the device: with the pool exhausted the step
-    backs nothing up and check_errors raises the allocator's RuntimeError (memory.py:62-66)."""
-    coord, pool = _his_coord(buf=8, top_k=4, ctx=64, host_pool=22)
-    coord.admit_request(0, 20, pool, torch.arange(1, 21, device=DEV))
-    reqs = torch.tensor([0], device=DEV)
-    for pos in (20, 21, 22):  # the first step is skipped, then two backups take the last 2 rows
-        coord.prepare_decode_step(reqs, torch.tensor([pos + 1], device=DEV))
+    backs nothing up and check_errors raises the allocator's RuntimeError (memory.py:62-66).
+    The previous token is still folded into the Quest bounds, as the reference folds it
+    (coordinator.py:204-208) before its alloc fails (:210): the bounds and counters equal
+    those of a coordinator whose pool has room, for both requests of the batch."""
+    coord, pool = _his_coord(buf=8, top_k=4, ctx=64, host_pool=42)
+    roomy, _ = _his_coord(buf=8, top_k=4, ctx=64, host_pool=200)
+    for c in (coord, roomy):
+        for r in (0, 1):
+            c.admit_request(r, 20, pool, torch.arange(1 + 64 * r, 21 + 64 * r, device=DEV))
+    reqs = torch.tensor([0, 1], device=DEV)
+    for pos in (20, 21):  # the first step is skipped, then one backup per request takes the last 2 rows
+        for c in (coord, roomy):
+            c.prepare_decode_step(reqs, torch.tensor([pos + 1, pos + 1], device=DEV))
+            for r in (0, 1):  # the token decoded at this step, in its hot-buffer slot
+                slot = r * 9 + min(pos, 8)
+                c.device_k[0][slot] = pool.k_all[0, 1 + 64 * r + pos]
+                c.device_v[0][slot] = pool.v_all[0, 1 + 64 * r + pos]
     coord.check_errors()
     assert coord.host_allocator.available_size() == 0
-    coord.prepare_decode_step(reqs, torch.tensor([24], device=DEV))  # position 22: no row left
+    for c in (coord, roomy):
+        c.prepare_decode_step(reqs, torch.tensor([23, 23], device=DEV))  # position 21: no row left in coord
     with pytest.raises(RuntimeError, match="out of memory"):
         coord.check_errors()
-    assert int(coord.req_to_host_pool[0, 22]) == -1 and int(coord.req_to_host_pool[0, 21]) >= 0
+    roomy.check_errors()
+    assert int(coord.req_to_host_pool[0, 21]) == -1 and int(coord.req_to_host_pool[1, 21]) == -1
+    assert int(coord.req_to_host_pool[0, 20]) >= 0 and int(roomy.req_to_host_pool[1, 21]) >= 0
+    qa, qb = coord.quest, roomy.quest
+    for name in ("page_k_bounds", "running_k_min", "running_k_max", "running_token_count", "running_page_idx"):
+        assert torch.equal(getattr(qa, name), getattr(qb, name)), name
 
 
 @pytest.mark.parametrize("fused", [True, False])
@@ -576,3 +593,70 @@ def test_quest_hisparse_step_in_a_graph_equals_eager():
         assert torch.equal(e[i], g[i]), what
     assert e[7] == g[7]
     assert int(e[6][1]) > 0  # the hot buffer swapped
+
+
+def test_swap_in_error_inside_a_replayed_graph_is_raised_by_the_poll():
+    """A position without host backup (coordinator.py:284-286) met inside a replayed decode
+    graph: no Python check runs during the replay, so the failed request shows as NaN outputs
+    in every layer while the other request's stay finite, and the backend's non-blocking poll
+    (poll_errors, the pinned error mirror) raises the reference's AssertionError once the
+    replay has finished; the next poll is clean.  Request 1's hot buffer is emptied and its
+    host rows cleared between two replays, so every position it selects is a miss without a
+    host row."""
+    from qwenquest_amd.attention.quest_hisparse import QuestHiSparseBackend
+    from qwenquest_amd.batch import ForwardBatch, ForwardMode
+    from qwenquest_amd.memory import MHATokenToKVPool, ReqToTokenPool
+
+    H4, KV4, D4, TOPK, PAGE, BUF, CTX, L4 = 32, 4, 128, 256, 64, 384, 1200, 2
+    prompts = (700, 1003)
+    rtp = ReqToTokenPool(2, CTX, DEV)
+    kvp = MHATokenToKVPool(2 * CTX, L4, KV4, D4, torch.bfloat16, DEV)
+    g = torch.Generator(device=DEV).manual_seed(71)
+    kvp.k_all.normal_(generator=g)
+    kvp.v_all.normal_(generator=g)
+    for r in (0, 1):
+        rtp.req_to_token[r] = torch.arange(1 + r * CTX, 1 + (r + 1) * CTX, dtype=torch.int32)
+    be = QuestHiSparseBackend(rtp, kvp, {"algorithm": "quest", "top_k": TOPK, "quest_page_size": PAGE,
+                                         "device_buffer_size": BUF}, host_pool_size=2 * CTX)
+    be.on_extend_finished(ForwardBatch(ForwardMode.EXTEND, None, None, torch.tensor([0, 1]),
+                                       torch.tensor(prompts), None, rtp, kvp, be))
+
+    class Lay:
+        def __init__(self, i):
+            self.layer_id, self.scaling = i, D4**-0.5
+
+    seq = torch.tensor([prompts[0] + 1, prompts[1] + 1], device=DEV, dtype=torch.int64)
+    batch = ForwardBatch(ForwardMode.DECODE, None, None, torch.tensor([0, 1], device=DEV), seq, None, rtp, kvp, be)
+    q_in = torch.randn(L4, 2, H4, D4, generator=g, device=DEV).to(torch.bfloat16)
+    k_in = torch.randn(L4, 2, KV4, D4, generator=g, device=DEV).to(torch.bfloat16)
+
+    def step():
+        be.init_forward_metadata(batch)
+        return [be.forward_decode(q_in[i], k_in[i], k_in[i], Lay(i), batch) for i in range(L4)]
+
+    for _ in range(2):  # eager steps first (workspaces, first-step skips)
+        step()
+        seq.add_(1)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = step()
+    graph.replay()
+    torch.cuda.synchronize()
+    be.poll_errors()  # a clean replay raises nothing
+    assert all(bool(torch.isfinite(o).all()) for o in outs)
+    seq.add_(1)
+    coord = be.coord
+    coord.buffer_tokens[:, 1] = -1
+    coord.req_to_host_pool[1] = -1
+    print("replay with request 1's host rows cleared", flush=True)
+    graph.replay()
+    torch.cuda.synchronize()
+    for i, o in enumerate(outs):
+        o = o.float().view(2, -1)
+        assert bool(torch.isnan(o[1]).all()), f"layer {i}: the failed request's output is not NaN"
+        assert bool(torch.isfinite(o[0]).all()), f"layer {i}: the other request's output is not finite"
+    with pytest.raises(AssertionError, match="without host backup"):
+        be.poll_errors()
+    be.poll_errors()  # raised once: the mirror is cleared
+    coord.check_errors()  # and so is the device word

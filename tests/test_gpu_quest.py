@@ -811,7 +811,7 @@ def test_decode_step_row_lookup():
     seq = torch.tensor([10, 5, 10, 1, 9, 9, 40], dtype=torch.int64, device=DEV)
     out = torch.full((rpi.numel(),), 99, dtype=torch.int64, device=DEV)
     _lib.call("qq_quest_decode_step_locs", _lib.ptr(rpi), _lib.ptr(seq), rpi.numel(), _lib.ptr(skip), _lib.ptr(r2t),
-              R, W, _lib.ptr(out), _lib.stream(DEV))
+              R, W, W, _lib.ptr(out), _lib.stream(DEV))
     torch.cuda.synchronize()
     t = r2t.cpu().long()
     expected = [-1, -1, -1, int(t[1, 0]), -1, -1, -1]  # r 0 and 2 skipped; r 1 at p = 0; r 5, -1 outside; p 38 >= W
@@ -819,6 +819,15 @@ def test_decode_step_row_lookup():
     assert skip.cpu().tolist() == [0, 0, 0, 1]
     skip.zero_()
     _lib.call("qq_quest_decode_step_locs", _lib.ptr(rpi[:2]), _lib.ptr(seq[:2]), 2, _lib.ptr(skip), _lib.ptr(r2t),
-              R, W, _lib.ptr(out), _lib.stream(DEV))
+              R, W, W, _lib.ptr(out), _lib.stream(DEV))
     torch.cuda.synchronize()
     assert out[:2].cpu().tolist() == [int(t[0, 8]), int(t[2, 3])]
+    # a view of the first 6 columns of the table: positions past its width give -1, not the
+    # next row's entries
+    view = r2t[:, :6]
+    seq2 = torch.tensor([8, 8, 7, 3], dtype=torch.int64, device=DEV)  # p = 6, 6, 5, 1
+    rpi2 = torch.tensor([0, 1, 2, 3], dtype=torch.int64, device=DEV)
+    _lib.call("qq_quest_decode_step_locs", _lib.ptr(rpi2), _lib.ptr(seq2), 4, _lib.ptr(skip), _lib.ptr(view),
+              R, view.shape[1], view.stride(0), _lib.ptr(out), _lib.stream(DEV))
+    torch.cuda.synchronize()
+    assert out[:4].cpu().tolist() == [-1, -1, int(t[2, 5]), int(t[3, 1])]

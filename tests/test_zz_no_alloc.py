@@ -40,46 +40,97 @@ def _setup(H, KV, D, P, TOP_K, CTX, prompts):
     return rtp, kvp, be
 
 
-def _call(lib, noalloc, be, rtp, kvp, H, reqs, seqs, seed):
-    """One layer through either entry point; returns (positions, out) after a sync."""
+def _inputs(be, rtp, kvp, H, reqs, seqs, seed):
+    """One layer's inputs, the step layout (prepare_step) and the output buffers (positions
+    -7, outputs 3.0), kept alive in a dict; "head" is the argument list both entry points
+    share."""
     from qwenquest_amd import _lib
 
     quest = be.quest
     bs = len(reqs)
     D, KV = kvp.head_dim, kvp.kv_heads
     g = torch.Generator(device=DEV).manual_seed(seed)
-    q = torch.randn((bs, H, D), generator=g, device=DEV).to(torch.bfloat16)
-    kn = torch.randn((bs, KV * D), generator=g, device=DEV).to(torch.bfloat16)
-    vn = torch.randn((bs, KV * D), generator=g, device=DEV).to(torch.bfloat16)
-    rpi = torch.tensor(reqs, device=DEV, dtype=torch.int64)
+    t = {}
+    t["q"] = torch.randn((bs, H, D), generator=g, device=DEV).to(torch.bfloat16)
+    t["kn"] = torch.randn((bs, KV * D), generator=g, device=DEV).to(torch.bfloat16)
+    t["vn"] = torch.randn((bs, KV * D), generator=g, device=DEV).to(torch.bfloat16)
+    t["rpi"] = torch.tensor(reqs, device=DEV, dtype=torch.int64)
     seq = torch.tensor(seqs, device=DEV, dtype=torch.int64)
-    loc = (1 + rpi * rtp.max_context_len + seq - 1).contiguous()
-    step = quest.prepare_step(seq)
-    positions = torch.full((bs, quest.top_k), -7, dtype=torch.int32, device=DEV)
-    out = torch.full((bs, H * D), 3.0, dtype=torch.bfloat16, device=DEV)
+    t["loc"] = (1 + t["rpi"] * rtp.max_context_len + seq - 1).contiguous()
+    t["step"] = step = quest.prepare_step(seq)
+    t["positions"] = torch.full((bs, quest.top_k), -7, dtype=torch.int32, device=DEV)
+    t["out"] = torch.full((bs, H * D), 3.0, dtype=torch.bfloat16, device=DEV)
     k_buf, v_buf = kvp.get_kv_buffer(0)
     r2t = rtp.req_to_token
-    head = [
-        _lib.ptr(q), _lib.DTYPE_BF16, q.stride(0), H, _lib.ptr(kn), _lib.ptr(vn), _lib.DTYPE_BF16,
-        _lib.ptr(loc), _lib.ptr(k_buf), _lib.ptr(v_buf), _lib.DTYPE_BF16, k_buf.shape[0],
-        _lib.ptr(quest.page_k_bounds), 0, _lib.ptr(rpi), _lib.ptr(step.seq_lens),
+    t["head"] = [
+        _lib.ptr(t["q"]), _lib.DTYPE_BF16, t["q"].stride(0), H, _lib.ptr(t["kn"]), _lib.ptr(t["vn"]), _lib.DTYPE_BF16,
+        _lib.ptr(t["loc"]), _lib.ptr(k_buf), _lib.ptr(v_buf), _lib.DTYPE_BF16, k_buf.shape[0],
+        _lib.ptr(quest.page_k_bounds), 0, _lib.ptr(t["rpi"]), _lib.ptr(step.seq_lens),
         _lib.ptr(step.candidate_limit_i32), _lib.ptr(step.actual_lens), bs, quest.max_reqs,
         quest.max_pages_per_req, KV, D, quest.page_size, quest.top_k, _lib.ptr(r2t), r2t.stride(0),
         r2t.shape[0], float(D**-0.5),
     ]
+    return t
+
+
+def _launch(lib, noalloc, t, H, KV, D, quest):
+    """Enqueue one call of either entry point on the current stream (no synchronisation)."""
+    from qwenquest_amd import _lib
+
+    bs = t["q"].shape[0]
     stream = _lib.stream(DEV)
     if noalloc:
-        st = lib.qq_quest_forward_decode_noalloc(*head, _lib.ptr(positions), _lib.ptr(out), stream)
+        st = lib.qq_quest_forward_decode_noalloc(*t["head"], _lib.ptr(t["positions"]), _lib.ptr(t["out"]), stream)
     else:
-        scores = torch.empty((bs, quest.max_pages_per_req), dtype=torch.float32, device=DEV)
-        ws = torch.empty(int(lib.qq_decode_attention_workspace_bytes(bs, quest.top_k, H, D)),
-                         dtype=torch.uint8, device=DEV)
-        sync = torch.zeros(int(lib.qq_quest_layer_step_sync_bytes(bs, KV)), dtype=torch.uint8, device=DEV)
-        st = lib.qq_quest_forward_decode(*head, _lib.ptr(scores), _lib.ptr(positions), _lib.ptr(out),
-                                         _lib.ptr(ws), ws.numel(), _lib.ptr(sync), sync.numel(), stream)
+        t["scores"] = torch.empty((bs, quest.max_pages_per_req), dtype=torch.float32, device=DEV)
+        t["ws"] = torch.empty(int(lib.qq_decode_attention_workspace_bytes(bs, quest.top_k, H, D)),
+                              dtype=torch.uint8, device=DEV)
+        t["sync"] = torch.zeros(int(lib.qq_quest_layer_step_sync_bytes(bs, KV)), dtype=torch.uint8, device=DEV)
+        st = lib.qq_quest_forward_decode(*t["head"], _lib.ptr(t["scores"]), _lib.ptr(t["positions"]),
+                                         _lib.ptr(t["out"]), _lib.ptr(t["ws"]), t["ws"].numel(), _lib.ptr(t["sync"]),
+                                         t["sync"].numel(), stream)
     _lib.check(st)
+
+
+def _call(lib, noalloc, be, rtp, kvp, H, reqs, seqs, seed):
+    """One layer through either entry point; returns (positions, out) after a sync."""
+    t = _inputs(be, rtp, kvp, H, reqs, seqs, seed)
+    _launch(lib, noalloc, t, H, kvp.kv_heads, kvp.head_dim, be.quest)
     torch.cuda.synchronize()
-    return positions.cpu(), out.cpu()
+    return t["positions"].cpu(), t["out"].cpu()
+
+
+def test_noalloc_first_call_inside_a_graph_capture():
+    """The process's first call of the entry point (the scratch address lookup and the
+    counter clear) made while a HIP graph is being captured: every replay, with eager work
+    and synchronisations between them, gives the workspace entry point's positions and
+    outputs bit for bit, and so does an eager call afterwards.  (No other test calls this
+    entry point before it: this file is collected last and this test comes first in it.)"""
+    from qwenquest_amd import _lib
+
+    lib = _lib.load()
+    H, KV, D, P, TOP_K, CTX, prompts = SHAPES[0]
+    rtp, kvp, be = _setup(H, KV, D, P, TOP_K, CTX, prompts)
+    reqs, seqs = [0, 1, 2, 3], [p + 1 for p in prompts]
+    pos_ref, out_ref = _call(lib, False, be, rtp, kvp, H, reqs, seqs, 5)
+    t = _inputs(be, rtp, kvp, H, reqs, seqs, 5)
+    torch.cuda.synchronize()
+    print("capture: first noalloc call inside torch.cuda.graph", flush=True)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        _launch(lib, True, t, H, KV, D, be.quest)
+    for rep in range(3):
+        t["positions"].fill_(-7)
+        t["out"].fill_(3.0)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(t["positions"].cpu(), pos_ref), f"replay {rep}: positions differ"
+        assert torch.equal(t["out"].cpu().view(torch.int16), out_ref.view(torch.int16)), f"replay {rep}: outputs differ"
+        _call(lib, False, be, rtp, kvp, H, [3, 1], [prompts[3] + 2, prompts[1] + 2], 6)  # eager work between
+    pos, out = _call(lib, True, be, rtp, kvp, H, reqs, seqs, 5)
+    assert torch.equal(pos, pos_ref) and torch.equal(out.view(torch.int16), out_ref.view(torch.int16))
+    del g
 
 
 @pytest.mark.parametrize("shape", range(len(SHAPES)))
@@ -97,6 +148,25 @@ def test_noalloc_matches_workspace_entry_point(shape):
         assert torch.equal(pos, pos_ref), f"positions differ (batch {len(reqs)})"
         assert torch.equal(out.view(torch.int16), out_ref.view(torch.int16)), f"outputs differ (batch {len(reqs)})"
         assert not torch.equal(out_ref, torch.full_like(out_ref, 3.0))
+
+
+def test_noalloc_takes_four_launch_batches_past_the_counter_region():
+    """The hand-off counters (64 KiB of the array) serve only the fused layer step (4 KV
+    heads): a four-launch shape whose batch would need more counters than that (80 requests
+    x 8 KV heads x 128 B = 80 KiB) is accepted and equals the workspace entry point."""
+    from qwenquest_amd import _lib
+
+    lib = _lib.load()
+    H, KV, D, P, TOP_K, CTX = 8, 8, 64, 16, 128, 400
+    prompts = [200 + 3 * i for i in range(80)]
+    assert 80 * KV * 128 > 64 << 10
+    rtp, kvp, be = _setup(H, KV, D, P, TOP_K, CTX, prompts)
+    reqs, seqs = list(range(80)), [p + 1 for p in prompts]
+    print(f"four-launch shape, batch {len(reqs)}", flush=True)
+    pos_ref, out_ref = _call(lib, False, be, rtp, kvp, H, reqs, seqs, 9)
+    pos, out = _call(lib, True, be, rtp, kvp, H, reqs, seqs, 9)
+    assert torch.equal(pos, pos_ref)
+    assert torch.equal(out.view(torch.int16), out_ref.view(torch.int16))
 
 
 def test_noalloc_rejects_sizes_beyond_its_scratch():
