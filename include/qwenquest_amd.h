@@ -419,6 +419,14 @@ int qq_hisparse_write_new_token(void* device_k_layer, void* device_v_layer, int 
 /* Device-side address of pinned host memory (hipHostGetDevicePointer). */
 int qq_host_device_pointer(void* host_ptr, void** device_ptr);
 
+/* Replaces the allocation of the reference's host tier (host_k / host_v,
+ * src/qwenquest/hisparse/coordinator.py:104-110, torch.zeros on the host device):
+ * `bytes` of pinned host memory at exactly that size (hipHostMalloc, default flags:
+ * mapped into the device's address space), contents undefined; QQ_EHIP when the
+ * system cannot pin that much.  qq_host_free releases it. */
+int qq_host_alloc(int64_t bytes, void** host_ptr);
+int qq_host_free(void* host_ptr);
+
 #ifdef __cplusplus
 }
 #endif

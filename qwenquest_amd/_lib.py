@@ -96,6 +96,8 @@ SIGNATURES: dict[str, tuple] = {
     "qq_hisparse_ring_free": (_I, [_P, _P, _L, _P, _L, _P]),
     "qq_hisparse_write_new_token": (_I, [_P, _P, _I, _P, _P, _I, _P, _P, _I, _I, _I, _L, _P]),
     "qq_host_device_pointer": (_I, [_P, ctypes.POINTER(ctypes.c_void_p)]),
+    "qq_host_alloc": (_I, [_L, ctypes.POINTER(ctypes.c_void_p)]),
+    "qq_host_free": (_I, [_P]),
 }
 
 _lib: ctypes.CDLL | None = None

@@ -939,7 +939,7 @@ static int forward_decode(
   QQ_REQUIRE(phase >= 1 && phase <= 3, "%s: phase %d is not 1, 2 or 3", what, phase);
   if (bs == 0) return QQ_OK;
 
-  SelectArgs sa;
+  SelectArgs sa{};
   sa.q = q;
   sa.q_dtype = q_dtype;
   sa.q_bstride = q_batch_stride;

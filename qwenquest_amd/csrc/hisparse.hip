@@ -957,6 +957,29 @@ extern "C" int qq_hisparse_write_new_token(void* device_k_layer, void* device_v_
   return check_launch("qq_hisparse_write_new_token");
 }
 
+// The host tier's pinned memory at its exact size (the reference's host_k / host_v,
+// torch.zeros on the host device, coordinator.py:104-110): hipHostMalloc with the
+// default flags (pinned, mapped into the device's address space), contents undefined.
+extern "C" int qq_host_alloc(int64_t bytes, void** host_ptr) {
+  QQ_REQUIRE(bytes > 0 && host_ptr, "qq_host_alloc: bad arguments");
+  *host_ptr = nullptr;
+  const hipError_t e = hipHostMalloc(host_ptr, (size_t)bytes, hipHostMallocDefault);
+  if (e != hipSuccess || !*host_ptr) {
+    (void)hipGetLastError();
+    *host_ptr = nullptr;
+    return set_error(QQ_EHIP, "qq_host_alloc: hipHostMalloc of %lld bytes failed: %s", (long long)bytes,
+                     hipGetErrorString(e));
+  }
+  return QQ_OK;
+}
+
+extern "C" int qq_host_free(void* host_ptr) {
+  if (!host_ptr) return QQ_OK;
+  const hipError_t e = hipHostFree(host_ptr);
+  if (e != hipSuccess) return set_error(QQ_EHIP, "qq_host_free: %s", hipGetErrorString(e));
+  return QQ_OK;
+}
+
 extern "C" int qq_host_device_pointer(void* host_ptr, void** device_ptr) {
   QQ_REQUIRE(host_ptr && device_ptr, "qq_host_device_pointer: null pointer");
   const hipError_t e = hipHostGetDevicePointer(device_ptr, host_ptr, 0);

@@ -545,7 +545,7 @@ extern "C" int qq_quest_retrieve_topk(const void* q, int q_dtype, int64_t q_batc
   QQ_REQUIRE(k_sel <= kMaxSel, "qq_quest_retrieve_topk: %d selected pages exceed %d", k_sel, kMaxSel);
   QQ_REQUIRE(bs >= 0 && layer >= 0 && max_pages >= 0, "qq_quest_retrieve_topk: bad sizes");
   if (bs == 0) return QQ_OK;
-  SelectArgs a;
+  SelectArgs a{};
   a.q = q;
   a.q_dtype = q_dtype;
   a.q_bstride = q_batch_stride;

@@ -32,9 +32,42 @@ from qwenquest_amd import _lib
 from qwenquest_amd.memory import MHATokenToKVPool, kv_pair_zeros
 from qwenquest_amd.quest import QuestAlgorithm
 
-__all__ = ["DeviceRowAllocator", "HiSparseCoordinator", "SwapInStats"]
+__all__ = ["DeviceRowAllocator", "HiSparseCoordinator", "SwapInStats", "pinned_zeros"]
 
 _ERR_VICTIMS, _ERR_HOST_ROW, _ERR_HOST_OOM = 1, 2, 4
+
+
+class _PinnedBlock:
+    """One block of pinned host memory from qq_host_alloc, released when the last tensor
+    viewing it is gone."""
+
+    def __init__(self, nbytes: int):
+        self.ptr = 0
+        ptr = ctypes.c_void_p()
+        _lib.call("qq_host_alloc", nbytes, ctypes.byref(ptr))
+        self.ptr, self.nbytes = int(ptr.value), nbytes
+        self._free = _lib.load().qq_host_free
+
+    def __del__(self):
+        if self.ptr:
+            self._free(ctypes.c_void_p(self.ptr))
+            self.ptr = 0
+
+
+def pinned_zeros(shape: tuple[int, ...], dtype: torch.dtype) -> torch.Tensor:
+    """A zeroed host tensor in pinned memory of exactly its size.  torch's pinned allocator
+    rounds every allocation up to a power of two, so a 48-layer host tier of 2 x 102 GiB
+    (batch 16 x 128K) would pin 2 x 128 GiB; this one pins what the tier holds."""
+    elems = 1
+    for d in shape:
+        elems *= int(d)
+    nbytes = elems * torch.tensor([], dtype=dtype).element_size()
+    block = _PinnedBlock(max(nbytes, 1))
+    arr = (ctypes.c_uint8 * block.nbytes).from_address(block.ptr)
+    arr._block = block  # the memory lives as long as any tensor viewing arr
+    t = torch.frombuffer(arr, dtype=torch.uint8)[:nbytes].view(dtype).view(shape)
+    t.zero_()
+    return t
 
 
 class DeviceRowAllocator:
@@ -134,8 +167,8 @@ class HiSparseCoordinator:
 
         # ---- host tier (pinned), full history of every request (rows from host_allocator)
         hshape = (num_layers, host_pool_size + 1, kv_heads, head_dim)
-        self.host_k_all = torch.zeros(hshape, dtype=dtype, pin_memory=True)
-        self.host_v_all = torch.zeros(hshape, dtype=dtype, pin_memory=True)
+        self.host_k_all = pinned_zeros(hshape, dtype)
+        self.host_v_all = pinned_zeros(hshape, dtype)
         self.host_k = list(self.host_k_all.unbind(0))
         self.host_v = list(self.host_v_all.unbind(0))
         self._host_k_dev = self._device_address(self.host_k_all)
