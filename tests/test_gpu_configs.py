@@ -8,9 +8,10 @@ heads x 128, bf16, page 64, top_k 2048 = 31 selected pages + the recent 64):
   both overlap modes, quest and quest_hisparse.
 
 Inputs are generated on the device from fixed seeds and copied to the host for the
-oracle; positions are compared bit for bit, attention within the bf16 tolerance of tests.conftest.attn_tol.  Where the
-oracle would need the whole batch in host memory (the 48-layer sweep) it follows sampled
-(layer, request) pairs from their own K rows.
+oracle; positions are compared bit for bit, attention within the bf16 tolerance of tests.conftest.attn_tol.  The
+48-layer sweep checks the prefill bounds of every (layer, request) on the device against the
+min / max of its K rows (exact operations) and starts the oracle from them, so that the oracle
+follows every pair without copying the whole K pool to the host.
 """
 
 from __future__ import annotations
@@ -115,13 +116,47 @@ def test_batch8_32k_per_page_offsets():
             assert_attn_close(out[i], ref, f"step {step} request {i}")
 
 
-def test_ragged_48_layer_sweep_sampled():
+SENT_MIN = int(np.array([bf16.BF16_MAX_BITS], dtype=np.uint16).view(np.int16)[0])  # unset page minimum
+SENT_MAX = int(np.array([bf16.BF16_MIN_BITS], dtype=np.uint16).view(np.int16)[0])  # unset page maximum
+
+
+def check_prefill_state_on_device(qs, k_all, starts, prompts):
+    """The backend's bounds after the prefill against their definition (quest.py:231-280),
+    on the device for every (layer, request): each complete page's (min, max) over its 64 K
+    rows, the partial page's running (min, max), the unset sentinels everywhere else, and the
+    page / token counters.  min and max are exact, so the comparison is bit for bit."""
+    L = qs.page_k_bounds.shape[0]
+    for r, n in enumerate(prompts):
+        full, part = divmod(int(n), P)
+        assert int(qs.running_page_idx[r]) == full and int(qs.running_token_count[r]) == part, f"request {r}"
+        for layer in range(L):
+            rows = k_all[layer, int(starts[r]) : int(starts[r]) + int(n)]
+            paged = rows[: full * P].view(full, P, KV, D)
+            pkb = qs.page_k_bounds[layer, r].view(torch.int16)
+            rmin = qs.running_k_min[layer, r].view(torch.int16)
+            rmax = qs.running_k_max[layer, r].view(torch.int16)
+            what = f"layer {layer} request {r}"
+            assert torch.equal(pkb[:full, ..., 0], paged.amin(1).view(torch.int16)), what
+            assert torch.equal(pkb[:full, ..., 1], paged.amax(1).view(torch.int16)), what
+            assert bool((pkb[full:, ..., 0] == SENT_MIN).all()) and bool((pkb[full:, ..., 1] == SENT_MAX).all()), what
+            if part:
+                assert torch.equal(rmin, rows[full * P :].amin(0).view(torch.int16)), what
+                assert torch.equal(rmax, rows[full * P :].amax(0).view(torch.int16)), what
+            else:
+                assert bool((rmin == SENT_MIN).all()) and bool((rmax == SENT_MAX).all()), what
+
+
+def test_ragged_48_layer_sweep_every_pair():
     """48 layers, batch 16, contexts uniform in [8192, 131072] (seeded), 64 decode steps with
-    one append per request per step, all layers through QuestOnlyBackend.  Sampled
-    (layer, request) pairs - every request in one layer, 19 pairs - follow the oracle from
-    their own K rows: positions bit-exact at every step, attention within attn_tol at sampled
-    steps, and the pair's page bounds / running bounds bit-exact after the last step (pages
-    completed during the sweep included)."""
+    one append per request per step, all layers through QuestOnlyBackend.  After the prefill,
+    every (layer, request)'s bounds are checked on the device against the min / max of its own
+    K rows; the oracle then starts from that state and follows all 768 (layer, request) pairs
+    itself: every step's new K / V rows in the pool bit-exact for every pair; positions
+    bit-exact for every pair at steps 0, 16, 31, 47 and 63, and for 19 sampled pairs (every
+    request in one layer, the longest and the shortest request, request 5 in layer 47) at every
+    step; attention within attn_tol for every pair at those five steps and for the sampled
+    pairs at steps 1 and 62; after the last step every pair's page bounds, running bounds and the
+    counters bit-exact (pages completed during the sweep included)."""
     from qwenquest_amd.attention.quest_only import QuestOnlyBackend
     from qwenquest_amd.batch import ForwardBatch, ForwardMode
     from qwenquest_amd.memory import MHATokenToKVPool, ReqToTokenPool
@@ -137,6 +172,7 @@ def test_ragged_48_layer_sweep_sampled():
     rtp = ReqToTokenPool(B, ctx, DEV)
     kvp = MHATokenToKVPool(pool, L, KV, D, torch.bfloat16, DEV)
     be = QuestOnlyBackend(rtp, kvp, {"algorithm": "quest", "top_k": TOP_K, "quest_page_size": P})
+    qs = be.quest
     base = torch.tensor(starts, device=DEV, dtype=torch.int64)
     rtp.req_to_token.copy_((base[:, None] + torch.arange(ctx, device=DEV)[None]).clamp(max=pool).to(torch.int32))
     for layer in range(L):
@@ -144,20 +180,23 @@ def test_ragged_48_layer_sweep_sampled():
         kvp.v_all[layer].copy_(dev_randn((pool + 1, KV, D), 2000 + layer).to(torch.bfloat16))
     prompts = [int(c) - 1 for c in ctxs]  # the first decode step has seq_len = ctxs[r]
     for r in range(B):
-        be.quest.update_prefill_representations_fused(r, kvp.k_all, rtp.req_to_token[r, : prompts[r]])
+        qs.update_prefill_representations_fused(r, kvp.k_all, rtp.req_to_token[r, : prompts[r]])
         be._skip_first_decode_update[r] = True
-    # every request in one layer (spread over the 48), plus the longest request in layer 0,
-    # the shortest in layer 23 and request 5 in layer 47
+    check_prefill_state_on_device(qs, kvp.k_all, starts, prompts)
+    st = oq.QuestState(TOP_K, P)
+    st.init_storage(0, L, B, ctx, KV, D)
+    assert st.page_k_bounds.shape == tuple(qs.page_k_bounds.shape)
+    for layer in range(L):
+        st.page_k_bounds[layer] = bf16_bits(qs.page_k_bounds[layer])
+    st.running_k_min[...] = bf16_bits(qs.running_k_min)
+    st.running_k_max[...] = bf16_bits(qs.running_k_max)
+    st.running_token_count[:] = qs.running_token_count.cpu().numpy()
+    st.running_page_idx[:] = qs.running_page_idx.cpu().numpy()
     samples = sorted({(7 * r % L, r) for r in range(B)} | {(0, int(np.argmax(ctxs))), (23, int(np.argmin(ctxs))),
                                                           (47, 5)})
-    oracles = {}
-    for layer, r in samples:
-        st = oq.QuestState(TOP_K, P)
-        st.init_storage(layer, layer + 1, 1, ctx, KV, D)
-        rows = int(starts[r]) + torch.arange(prompts[r], device=DEV)
-        st.update_prefill_representations(layer, 0, bf16_bits(kvp.k_all[layer, rows]), np.arange(prompts[r]))
-        oracles[(layer, r)] = st
-    check_steps = {0, 1, 31, 62, 63}
+    every_pair_steps = {0, 16, 31, 47, 63}
+    sampled_attention_steps = {1, 62}
+    reqs = np.arange(B)
     seq = torch.tensor(ctxs, device=DEV, dtype=torch.int64)
     loc = torch.empty(B, device=DEV, dtype=torch.int64)
     batch = ForwardBatch(ForwardMode.DECODE, None, None, torch.arange(B, device=DEV), seq, loc, rtp, kvp, be)
@@ -168,35 +207,58 @@ def test_ragged_48_layer_sweep_sampled():
         vn = dev_randn((L, B, KV, D), 4000 + step).to(torch.bfloat16)
         q = dev_randn((L, B, H, D), 5000 + step).to(torch.bfloat16)
         seqs = seq.cpu().numpy()
-        for (layer, r), st in oracles.items():
-            if step > 0:  # fold the previous decode token (its K arrived through forward_decode)
-                prev = bf16_bits(kvp.k_all[layer, int(base[r]) + int(seqs[r]) - 2][None])
-                st.update_decode_representations(layer, [0], prev, [0])
-                st.maybe_finalize_decode_representations([0])
-            st.prepare_step(seqs[r : r + 1])
+        if step > 0:  # fold the previous decode token of every pair (checked in the pool last step)
+            prev = bf16_bits(kvp.k_all[:, base + seq - 2])  # [L, B, KV, D]
+            for layer in range(L):
+                st.update_decode_representations(layer, reqs, prev[layer], reqs)
+            st.maybe_finalize_decode_representations(reqs)
+        st.prepare_step(seqs)
+        every = step in every_pair_steps
         for layer in range(L):
             out = be.forward_decode(q[layer], kn[layer], vn[layer], Layer(layer), batch)
-            for (sl, r), st in oracles.items():
-                if sl != layer:
-                    continue
-                pos = be._positions[r].cpu().numpy()
-                ref_pos, ref_actual, _ = st.retrieve_topk(q[layer, r : r + 1].float().cpu().numpy(), layer, [0])
-                n = int(ref_actual[0])
-                assert np.array_equal(pos[:n], ref_pos[0, :n]), f"step {step} layer {layer} request {r}"
-                if step not in check_steps:
-                    continue
-                rows = (int(base[r]) + torch.from_numpy(ref_pos[0, :n].astype(np.int64))).to(DEV)
-                ref = oracle_attention(q[layer, r].cpu(), kvp.k_all[layer, rows].cpu(), kvp.v_all[layer, rows].cpu())
-                assert_attn_close(out[r].float().cpu().numpy(), ref, f"step {step} layer {layer}")
+            mine = [r for (sl, r) in samples if sl == layer]
+            if not every and not mine:
+                continue
+            pos = be._positions[:B].cpu().numpy()
+            qf = q[layer].float().cpu().numpy()
+            if every:
+                ref_pos, ref_actual, _ = st.retrieve_topk(qf, layer, reqs)
+                check = list(range(B))
+            else:
+                ref_pos = np.zeros((B, TOP_K), dtype=np.int32)
+                ref_actual = np.zeros(B, dtype=np.int32)
+                for r in mine:
+                    lay = oq.step_layout(seqs[r : r + 1], P, TOP_K, False)
+                    qbar = oq.group_queries(qf[r : r + 1], KV, D, True)
+                    p1, a1, _ = oq.retrieve_topk(qbar, st.page_k_bounds[layer, [r]], lay, P, TOP_K)
+                    ref_pos[r], ref_actual[r] = p1[0], a1[0]
+                check = mine
+            for r in check:
+                n = int(ref_actual[r])
+                assert n == TOP_K
+                assert np.array_equal(pos[r, :n], ref_pos[r, :n]), f"step {step} layer {layer} request {r}"
+            attend = check if every else (mine if step in sampled_attention_steps else [])
+            if not attend:
+                continue
+            outs = out.float().cpu().numpy()
+            rows = (base[attend][:, None] + torch.from_numpy(ref_pos[attend].astype(np.int64)).to(DEV))
+            kr, vr = kvp.k_all[layer, rows].cpu(), kvp.v_all[layer, rows].cpu()
+            qc = q[layer].cpu()
+            for j, r in enumerate(attend):
+                ref = oracle_attention(qc[r], kr[j], vr[j])
+                assert_attn_close(outs[r], ref, f"step {step} layer {layer} request {r}")
+        # the step's new token of every pair, as set_kv_buffer stored it (memory.py:114-120)
+        assert torch.equal(kvp.k_all[:, loc].view(torch.int16), kn.view(torch.int16)), f"step {step}"
+        assert torch.equal(kvp.v_all[:, loc].view(torch.int16), vn.view(torch.int16)), f"step {step}"
         seq.add_(1)
     torch.cuda.synchronize()
-    for (layer, r), st in oracles.items():
-        assert np.array_equal(bf16_bits(be.quest.page_k_bounds[layer, r]), st.page_k_bounds[0, 0])
-        assert np.array_equal(bf16_bits(be.quest.running_k_min[layer, r]), st.running_k_min[0, 0])
-        assert np.array_equal(bf16_bits(be.quest.running_k_max[layer, r]), st.running_k_max[0, 0])
-        assert int(be.quest.running_page_idx[r]) == int(st.running_page_idx[0])
-        assert int(be.quest.running_token_count[r]) == int(st.running_token_count[0])
-    del rtp, kvp, be
+    for layer in range(L):
+        assert np.array_equal(bf16_bits(qs.page_k_bounds[layer]), st.page_k_bounds[layer]), f"layer {layer}"
+    assert np.array_equal(bf16_bits(qs.running_k_min), st.running_k_min)
+    assert np.array_equal(bf16_bits(qs.running_k_max), st.running_k_max)
+    assert np.array_equal(qs.running_page_idx.cpu().numpy(), st.running_page_idx)
+    assert np.array_equal(qs.running_token_count.cpu().numpy(), st.running_token_count)
+    del rtp, kvp, be, qs
     torch.cuda.empty_cache()
 
 
