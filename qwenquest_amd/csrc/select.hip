@@ -235,6 +235,136 @@ __global__ __launch_bounds__(kThreads) void score_pages_fast_kernel(SelectArgs a
   }
 }
 
+// score_pages_fast_kernel at KV*D = 4*128 with bf16 queries and 2 <= G <= 8 (the
+// shape of the fused layer step), in a shape that reads the bounds faster: each
+// wave scores 4 pages, a 256-thread block 16, and the kernel fits 64 VGPRs, so
+// eight waves per SIMD hold every block of a batch of 16 at 128K at once (2048
+// blocks; 8 x 16-byte loads per lane in flight instead of 16).  Each load
+// instruction reads 1 KiB of a page: lane l holds words [4l, 4l + 4) of the page's
+// first half and of its second.  The canonical lane partials (lane L: channels
+// 8L .. 8L+7 summed in order) are rebuilt exactly: an even lane's four products
+// are the first half of an odd lane's sum, which continues it after one DPP move,
+// so odd lane 2m+1 holds the partials of canonical lanes m (first half) and m + 32
+// (second half).  Their sum is the tree's first level; the levels 16 .. 1 pair
+// odd lanes 32, 16, 8, 4 and 2 apart, the 4 pages' trees interleaved as in
+// reduce8_pages.  Lane 16p + 1 ends with page p's score, bit-identical to
+// score_8pages.  The query words of the GQA mean are loaded unconditionally (heads
+// past G re-read the last one and are not summed).  One extra block per request
+// (blockIdx.x == 0; page tiles follow it) stores the new token's K/V, so that its
+// registers are not held across the page loads.
+constexpr int kPagesPerBlock4 = 16;
+
+// v of lane l - 1 for odd lanes (quad_perm [0, 0, 2, 2])
+__device__ inline float lane_from_even(float v) { return dpp_f32<0xA0>(v); }
+
+// Canonical partial of one 16-byte piece of each half page (words [4l, 4l + 4) and
+// [256 + 4l, 256 + 4l + 4)), summed over both halves: valid in odd lanes.
+__device__ inline float half_pages_partial(const uint4 (&w)[2], const float4 (&q)[2]) {
+  float u = 0.0f;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint32_t ws[4] = {w[h].x, w[h].y, w[h].z, w[h].w};
+    const float qs[4] = {q[h].x, q[h].y, q[h].z, q[h].w};
+    float pr[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      pr[k] = __fmul_rn(qs[k], __uint_as_float(__builtin_amdgcn_perm(ws[k], ws[k], qs[k] >= 0.0f ? 0x03020C0Cu
+                                                                                                  : 0x01000C0Cu)));
+    const float first = __fadd_rn(__fadd_rn(__fadd_rn(pr[0], pr[1]), pr[2]), pr[3]);  // an even lane's 4
+    float t = lane_from_even(first);                                                 // odd lanes: continue it
+#pragma unroll
+    for (int k = 0; k < 4; ++k) t = __fadd_rn(t, pr[k]);
+    u = h == 0 ? t : __fadd_rn(u, t);  // tree level 32: canonical lanes m and m + 32
+  }
+  return u;
+}
+
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(8, 8)))
+void score_pages_fast4_kernel(SelectArgs a, int store_new) {
+  constexpr int C = 512, D = 128;
+  const int b = blockIdx.y;
+  if (blockIdx.x == 0) {  // the new token's block (its test needs no argument load)
+    if (store_new) store_new_token(a, b);
+    return;
+  }
+  // every argument of the scoring path in the first batch of argument loads; the
+  // request's three words go out together, and the query words (their addresses
+  // need only b) before the wait for them: one round trip before the page loads
+  // instead of a chain of three
+  __asm__ volatile("" ::"s"(a.top_k), "s"(a.k_sel), "s"(a.R), "s"(a.MP), "s"(a.bounds_layer), "s"(a.scores));
+  const int64_t s = a.seq[b];
+  const int limit = a.limit[b];
+  const int64_t req = a.rpi[b];
+  const int G = a.H / (C / D);
+  // channel pair (2t, 2t + 1) = head t >> 6, channels 2 (t & 63) .. +1
+  const int tid = threadIdx.x;
+  const uint32_t* qp = reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(a.q) + (int64_t)b * a.q_bstride +
+                                                         (int64_t)(tid >> 6) * G * D) + (tid & 63);
+  uint32_t qw[8];
+#pragma unroll
+  for (int g = 0; g < 8; ++g) qw[g] = qp[(int64_t)min(g, G - 1) * (D / 2)];
+  __asm__ volatile("" ::"s"(s), "s"(limit), "s"(req) : "memory");
+  const int lim = min(limit, a.MP);
+  const int p0 = (blockIdx.x - 1) * kPagesPerBlock4;
+  if (s <= a.top_k || a.k_sel == 0 || p0 >= lim || req < 0 || req >= a.R) return;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int pw = p0 + wave * 4;  // this wave's 4 pages
+  uint4 w[4][2];
+  {
+    const char* rb = reinterpret_cast<const char*>(a.bounds_layer + req * a.MP * C) + 16 * lane;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const char* page = rb + (int64_t)min(pw + i, lim - 1) * (C * 4);
+      w[i][0] = *reinterpret_cast<const uint4*>(page);
+      w[i][1] = *reinterpret_cast<const uint4*>(page + C * 2);
+    }
+  }
+  __shared__ __align__(16) float s_q[C];
+  {
+    float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+      if (g < G) {
+        a0 = __fadd_rn(a0, bf2f((uint16_t)(qw[g] & 0xFFFFu)));
+        a1 = __fadd_rn(a1, bf2f((uint16_t)(qw[g] >> 16)));
+      }
+    }
+    s_q[2 * tid] = bf2f(f2bf(a0 / (float)G));
+    s_q[2 * tid + 1] = bf2f(f2bf(a1 / (float)G));
+  }
+  lds_barrier();  // s_q is written; the page loads stay in flight
+  if (pw >= lim) return;
+  float4 q[2];
+  q[0] = *reinterpret_cast<const float4*>(&s_q[4 * lane]);
+  q[1] = *reinterpret_cast<const float4*>(&s_q[C / 2 + 4 * lane]);
+  float u[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) u[i] = half_pages_partial(w[i], q);
+  // tree levels 16 .. 1 over odd lanes, the 4 pages interleaved: after level 16 the
+  // lower half of the wave holds pages 0, 1 and the upper half pages 2, 3; after
+  // level 8 each 16-lane row holds one page
+  const bool up32 = lane & 32, up16 = lane & 16;
+  float v2[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const float send = up32 ? u[j] : u[2 + j];
+    const float keep = up32 ? u[2 + j] : u[j];
+    v2[j] = __fadd_rn(keep, lane_xor32(send, lane));
+  }
+  float v;
+  {
+    const float send = up16 ? v2[0] : v2[1];
+    const float keep = up16 ? v2[1] : v2[0];
+    v = __fadd_rn(keep, lane_xor16(send, lane));
+  }
+  v = __fadd_rn(v, lane_xor8(v));  // lanes 2m+1 and 2m+9 of the row
+  v = __fadd_rn(v, lane_up4(v));   // 2m+1 and 2m+5
+  v = __fadd_rn(v, lane_xor2(v));  // 1 and 3
+  const int p = pw + (lane >> 4);
+  if ((lane & 15) == 1 && p < lim) a.scores[(int64_t)b * a.MP + p] = v;
+}
+
 // One block per request: top k_sel pages (quest.py:450-452) + token layout (453-460).
 __global__ __launch_bounds__(kThreads) void select_layout_kernel(SelectArgs a) {
   const int b = blockIdx.x;
@@ -448,7 +578,11 @@ int launch_score(const SelectArgs& a, int bs, bool store_new, hipStream_t s) {
   dim3 grid(max(1, ceil_div(a.MP, kPagesPerBlock)), bs);
   const int M = (a.C + 63) / 64;
   const int st = store_new ? 1 : 0;
-  if (a.C == 512)
+  const int G = a.KV > 0 ? a.H / a.KV : 0;
+  if (a.C == 512 && a.D == 128 && a.q_dtype == QQ_DTYPE_BF16 && G >= 2 && G <= 8 && a.H == G * a.KV) {
+    const int tiles = max(1, ceil_div(a.MP, kPagesPerBlock4));
+    score_pages_fast4_kernel<<<dim3(tiles + 1, bs), kThreads, 0, s>>>(a, st);
+  } else if (a.C == 512)
     score_pages_fast_kernel<8><<<grid, kThreads, 0, s>>>(a, st);
   else if (a.C == 1024)
     score_pages_fast_kernel<16><<<grid, kThreads, 0, s>>>(a, st);

@@ -248,13 +248,16 @@ def test_page_scores_bit_exact_in_canonical_order(kv, d, dtype):
     assert np.array_equal(np.isneginf(got), np.isneginf(ref))
 
 
-@pytest.mark.parametrize("kv,d", [(4, 128), (8, 128), (4, 64), (2, 32), (5, 32), (3, 8)])
+@pytest.mark.parametrize("kv,d,group", [(4, 128, 4), (4, 128, 1), (4, 128, 2), (4, 128, 8), (4, 128, 16), (8, 128, 4),
+                                         (4, 64, 4), (2, 32, 4), (5, 32, 4), (3, 8, 4)])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-def test_retrieve_scores_bit_exact_in_canonical_order(kv, d, dtype):
+def test_retrieve_scores_bit_exact_in_canonical_order(kv, d, group, dtype):
     """The scores retrieve_topk ranks (its scoring launch, fused with the GQA mean) equal
     the oracle's bit for bit on every candidate page, for the 16-byte lane-load shapes
-    (KV*D = 256, 512, 1024) and the general ones; 3 requests of different limits."""
-    P, heads = 16, kv * 4
+    (KV*D = 256, 512, 1024; at 4 x 128 with bf16 queries and GQA groups of 2 .. 8 the
+    4-pages-per-wave kernel, other groups the general one) and the general shapes;
+    3 requests of different limits (partial page tiles)."""
+    P, heads = 16, kv * group
     q, st = new_quest(64, P, 1, 3, 4096, kv, d)
     pool = rand_bf16((4096, kv, d), seed=kv * d + 1, mean=rand_bf16((4096, 1, 1), seed=3, scale=0.5))
     lens = (4000, 1500, 700)
