@@ -57,6 +57,9 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 PROFILE = os.path.join(ROOT, "profiles", "quest_layer_step_kernels_b16_128k.md")
+# the layer step's two launches at the headline shape (KV*D = 4 x 128, bf16, GQA group 8)
+SCORE_KERNEL = "score_pages_fast4_kernel"
+ATTEND_KERNEL = "quest_attend_unit_kernel"
 
 
 def sources_sha16() -> str:
@@ -405,7 +408,7 @@ def quest_config(name: str, what: str, B: int, ctxs, L: int, warmup: int, steps:
                "layers": L, "steps": steps, "warmup": warmup, "us_per_layer_step": round(us, 2),
                "tokens_per_s": round(B / (ms * 1e-3), 1), "algorithmic_bytes_per_layer_step": byts["headline"],
                "hbm_frac": round(byts["headline"] / (us * 1e-6) / (HBM_PEAK_GBS * 1e9), 4),
-               "kernels_us": {"score_pages_fast_kernel": round(k_sel, 2), "quest_attend_unit_kernel": round(k_att, 2)}}
+               "kernels_us": {SCORE_KERNEL: round(k_sel, 2), ATTEND_KERNEL: round(k_att, 2)}}
         if cpu_reps > 0:
             res["cpu_baseline"] = run.cpu(cpu_reps)
             res["cpu_baseline"]["sample"] = (f"one whole layer-step (all {B} requests, layer 0 of the GPU's state), "
@@ -923,8 +926,8 @@ def measure_layouts(headline_us: float, B: int, S: int, L: int, warmup: int, ste
             k_sel, k_att = run.kernel_us()
             out[layout] = {"what": what, "us_per_layer_step": round(us, 2),
                            "delta_us_vs_contiguous": round(us - headline_us, 2),
-                           "kernels_us": {"score_pages_fast_kernel": round(k_sel, 2),
-                                          "quest_attend_unit_kernel": round(k_att, 2)}}
+                           "kernels_us": {SCORE_KERNEL: round(k_sel, 2),
+                                          ATTEND_KERNEL: round(k_att, 2)}}
             print(f"[bench] layout {layout}: {out[layout]['us_per_layer_step']} us per layer-step", file=sys.stderr,
                   flush=True)
         finally:
@@ -995,8 +998,8 @@ def main() -> int:
     us_sel, us_att = run.kernel_us()
     bw_sel = byts["bounds"] / (us_sel * 1e-6) / 1e9
     bw_att = byts["kv"] / (us_att * 1e-6) / 1e9
-    dominant = ("quest_attend_unit_kernel", us_att, byts["kv"], bw_att) if us_att >= us_sel else (
-        "score_pages_fast_kernel", us_sel, byts["bounds"], bw_sel)
+    dominant = (ATTEND_KERNEL, us_att, byts["kv"], bw_att) if us_att >= us_sel else (
+        SCORE_KERNEL, us_sel, byts["bounds"], bw_sel)
     cpu = None
     if args.cpu_reps > 0:
         cpu = run.cpu(args.cpu_reps)
@@ -1033,7 +1036,7 @@ def main() -> int:
         "hbm_frac_layer_step": round(step_frac, 4),
         "tokens_per_s": round(B / (ms_per_step * 1e-3), 1),
         "algorithmic_bytes_per_layer_step": byts,
-        "kernels_us": {"score_pages_fast_kernel": round(us_sel, 2), "quest_attend_unit_kernel": round(us_att, 2)},
+        "kernels_us": {SCORE_KERNEL: round(us_sel, 2), ATTEND_KERNEL: round(us_att, 2)},
         "roofline": {"kernel": dominant[0], "bound": "hbm", "achieved": round(dominant[3], 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(dominant[3] / HBM_PEAK_GBS, 4),
                      "traffic": None if (args.ragged or args.layout != "contiguous") else traffic.get(dominant[0]),
