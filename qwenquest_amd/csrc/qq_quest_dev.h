@@ -280,6 +280,31 @@ __device__ inline uint64_t dpp64(uint64_t v) {
   return ((uint64_t)hi << 32) | lo;
 }
 
+// The page whose score thread `tid` of an NT-thread selection holds in slot i.
+// The scores arrive in page blocks (page tid + NT i: coalesced loads).  The
+// selections take their threshold from the maxima of 64 groups of NT/64
+// consecutive threads; with fewer candidates than threads, page blocks leave
+// groups empty (127 candidates fill 16 of 64 groups at NT = 512), every key then
+// passes the threshold and the ranking takes its quadratic path.  Such a block
+// spreads its pages first: slot 0 moves through the LDS so that group g holds
+// pages g, g + 64, ... and the k-th largest group maximum stays a tight bound
+// (the other slots hold pages >= NT, past every candidate).
+template <int NT>
+__device__ inline int sel_page(int tid, int i, bool spread) {
+  constexpr int GS = NT / 64;
+  return spread ? NT * i + tid / GS + 64 * (tid % GS) : tid + NT * i;
+}
+
+// Slot 0's score after the spread (block-uniform `spread`; tmp: NT floats of LDS
+// that nothing reads or writes until the next block barrier).
+template <int NT>
+__device__ inline float spread_slot0(float v, bool spread, float* tmp) {
+  if (!spread) return v;
+  tmp[threadIdx.x] = v;
+  lds_barrier();
+  return tmp[sel_page<NT>(threadIdx.x, 0, true)];
+}
+
 template <int KPT, int NT = kBlock>
 struct SelectSmem {
   uint64_t cand[NT * KPT + 64];  // survivors, flattened (zero-padded up to 64)
@@ -293,7 +318,8 @@ struct SelectSmem {
 
 // Top k <= 64 pages of n_eff <= NT*KPT keys (quest.py:450-452), whole block of
 // NT threads: sv[i] is the score of page tid + NT i (pages >= lim rank as
-// -inf).  Keys are (order-preserving score, ~page), so "larger" = higher
+// -inf); a block with fewer candidates than threads spreads them first
+// (sel_page).  Keys are (order-preserving score, ~page), so "larger" = higher
 // score, then lower page, and all keys differ.
 //   1. tau = the k-th largest of the maxima of 64 groups of NT/64 threads (1
 //      when fewer than k groups hold keys).  The k largest group maxima are k
@@ -311,12 +337,14 @@ __device__ inline void select_topk_block(const float (&sv)[KPT], int lim, int n_
   constexpr int NW = NT / 64, GS = NT / 64, SHARE = 64 / NW;
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
+  const bool spread = lim < NT;  // block-uniform
+  const float s0 = spread_slot0<NT>(sv[0], spread, reinterpret_cast<float*>(s.cand));
   uint64_t key[KPT];
   uint64_t tmax = 0ull;
 #pragma unroll
   for (int i = 0; i < KPT; ++i) {
-    const int p = tid + NT * i;
-    key[i] = p < n_eff ? sel_key(p < lim ? orderable(sv[i]) : kNegInfKey, p) : 0ull;
+    const int p = sel_page<NT>(tid, i, spread);
+    key[i] = p < n_eff ? sel_key(p < lim ? orderable(i == 0 ? s0 : sv[i]) : kNegInfKey, p) : 0ull;
     tmax = key[i] > tmax ? key[i] : tmax;
   }
   // group maximum over GS consecutive lanes with DPP moves (no LDS round trips):
@@ -455,8 +483,9 @@ __device__ inline uint32_t wave_max_u32(uint32_t v, int lane) {
 }
 
 // Top k <= 64 pages of n_eff <= NT*KPT pages (quest.py:450-452) with an NT-thread
-// block (NT = 256 or 512): sv[i] is the score of page tid + NT i (pages >= lim rank
-// as -inf).  The order is (score desc, page asc): 64-bit keys (order-preserving
+// block (NT = 256 or 512): sv[i] is the score of page tid + NT i (pages >= lim
+// rank as -inf), spread first when there are fewer candidates than threads
+// (sel_page).  The order is (score desc, page asc): 64-bit keys (order-preserving
 // score, ~page), all distinct.  Every comparison pass is split over the block's
 // waves and handed over through LDS, 4 barriers in all:
 //   A. per thread the largest 32-bit score key of its pages, per group of NT/64
@@ -481,12 +510,14 @@ __device__ inline void select_ranked(const float (&sv)[KPT], int lim, int n_eff,
   constexpr int NW = NT / 64, SHARE = 64 / NW;
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = tid >> 6;
+  const bool spread = lim < NT;  // block-uniform
+  const float s0 = spread_slot0<NT>(sv[0], spread, reinterpret_cast<float*>(s.cand));
   uint32_t key[KPT];
   uint32_t tmax = 0u;
 #pragma unroll
   for (int i = 0; i < KPT; ++i) {
-    const int p = tid + NT * i;
-    const uint32_t o = orderable(sv[i]);
+    const int p = sel_page<NT>(tid, i, spread);
+    const uint32_t o = orderable(i == 0 ? s0 : sv[i]);
     key[i] = p < lim ? o : (p < n_eff ? kNegInfKey : 0u);  // 0: not a page (below every key)
     tmax = max(tmax, key[i]);
   }
@@ -524,7 +555,7 @@ __device__ inline void select_ranked(const float (&sv)[KPT], int lim, int n_eff,
     if (key[i] >= tau)
       s.cand[base + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask[i] >> 32),
                                                    __builtin_amdgcn_mbcnt_lo((uint32_t)mask[i], 0u))] =
-          sel_key(key[i], tid + NT * i);
+          sel_key(key[i], sel_page<NT>(tid, i, spread));
     base += __popcll(mask[i]);
   }
   lds_barrier();  // C

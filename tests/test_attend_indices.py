@@ -24,6 +24,7 @@ from __future__ import annotations
 import itertools
 import math
 
+import numpy as np
 import pytest
 
 # geometry of decode.hip (kept in step with its constants and host helpers)
@@ -143,13 +144,31 @@ def check_units(top_k, n, bs):
     return waves, parts
 
 
+def sel_page(tid, i, nt, spread=True):
+    """Page whose score thread tid holds in slot i (qq_quest_dev.h sel_page): page
+    blocks (page tid + nt*i, as the scores are loaded) or, spread (fewer candidates
+    than threads), page nt*i + g + 64*m with group g of nt/64 consecutive threads."""
+    gs = nt // 64
+    return nt * i + tid // gs + 64 * (tid % gs) if spread else tid + nt * i
+
+
+def kernel_page(tid, i, nt, lim):
+    """The mapping the selections use for a request with lim candidates."""
+    return sel_page(tid, i, nt, lim < nt)
+
+
 def check_selection(top_k, page, max_pages, lim, waves):
     nt = 64 * waves
     k = top_k // page - 1
     kpt = kpt_form(max_pages, k, nt)
     n_eff = max(lim, k)
     assert n_eff <= kpt * nt
-    # score reads clamp to the request's row of max_pages entries
+    # every page slot of the block is held by exactly one (thread, slot), in both mappings;
+    # the spread moves slot 0 only, inside the block's first nt pages
+    for spread in (False, True):
+        assert sorted(sel_page(t, i, nt, spread) for t in range(nt) for i in range(kpt)) == list(range(nt * kpt))
+    assert sorted(sel_page(t, 0, nt, True) for t in range(nt)) == list(range(nt))
+    # score reads (page blocks) clamp to the request's row of max_pages entries
     reads = {min(tid + nt * i, max_pages - 1) for tid in range(nt) for i in range(kpt)}
     assert max(reads) < max_pages and min(reads) >= 0
     assert k <= MAX_SEL
@@ -253,3 +272,85 @@ def test_model_catches_a_fill_of_the_real_slots_only():
     _, _, reads, _ = attend_block(n, 0, 32, 4, 16)
     written_real_only = set(range(n))
     assert not reads <= written_real_only
+
+
+# ------------------------------------------------------------- selection model
+# select_ranked / select_topk_block (qq_quest_dev.h) on the CPU: keys ordered by score,
+# then lower page; tau = the k-th largest maximum of 64 groups of nt/64 consecutive
+# threads; the keys >= tau survive and are ranked.  The model checks the two-stage
+# algorithm against an exact top-k (np.lexsort) and the survivor count that decides
+# between the 64-survivor ranking and the quadratic one.
+
+
+def model_select(scores, lim, n_eff, k, nt, kpt, mapping):
+    """(pages in rank order, survivor count) of the block selection; mapping(tid, i, nt)
+    gives the page a thread's slot holds."""
+    gs = nt // 64
+    keys = np.zeros((nt, kpt), dtype=object)
+    for tid in range(nt):
+        for i in range(kpt):
+            p = mapping(tid, i, nt)
+            if p < n_eff:
+                sc = scores[p] if p < lim else -np.inf
+                keys[tid, i] = (sc, -p)  # larger = higher score, then lower page
+            else:
+                keys[tid, i] = None  # not a page: below every key
+    def kmax(a, b):
+        if a is None:
+            return b
+        if b is None:
+            return a
+        return max(a, b)
+    gmax = []
+    for g in range(64):
+        m = None
+        for t in range(g * gs, (g + 1) * gs):
+            for i in range(kpt):
+                m = kmax(m, keys[t, i])
+        gmax.append(m)
+    real = sorted((m for m in gmax if m is not None), reverse=True)
+    tau = real[k - 1] if len(real) >= k else None  # None: every key survives
+    surv = [key for key in keys.flat if key is not None and (tau is None or key >= tau)]
+    surv.sort(reverse=True)
+    return [-key[1] for key in surv[:k]], len(surv)
+
+
+def exact_topk(scores, lim, n_eff, k):
+    sc = np.array([scores[p] if p < lim else -np.inf for p in range(n_eff)])
+    order = np.lexsort((np.arange(n_eff), -sc))  # score desc, page asc
+    return [int(p) for p in order[:k]]
+
+
+@pytest.mark.parametrize("lim,nt,kpt", [(31, 256, 2), (40, 256, 2), (63, 256, 2), (127, 256, 2), (127, 512, 2),
+                                        (255, 512, 2), (300, 256, 2), (1023, 512, 2), (2047, 512, 5)])
+def test_selection_model_matches_exact_topk(lim, nt, kpt):
+    rng = np.random.default_rng(lim * 7 + nt)
+    k = 31
+    n_eff = max(lim, k)
+    for trial in range(3):
+        scores = rng.standard_normal(lim).astype(np.float32)
+        if trial == 1:  # heavy ties: a few distinct values
+            scores = rng.integers(0, 4, lim).astype(np.float32)
+        pages, total = model_select(scores, lim, n_eff, k, nt, kpt, lambda t, i, n: kernel_page(t, i, n, lim))
+        assert pages == exact_topk(scores, lim, n_eff, k)
+        if trial == 0 and lim >= 64:
+            # distinct scores: the threshold keeps the ranking on its 64-survivor path
+            assert total <= 64, (lim, nt, total)
+
+
+def test_page_blocks_would_take_the_quadratic_ranking():
+    """Page blocks alone (page tid + nt*i) fill 16 of 64 groups with 127 candidates at
+    nt = 512: every key passes the threshold.  Spread, the same candidates keep the
+    ranking on its 64-survivor path; from nt candidates on, blocks fill every group."""
+    rng = np.random.default_rng(5)
+    scores = rng.standard_normal(127).astype(np.float32)
+    block = lambda tid, i, nt: sel_page(tid, i, nt, False)  # noqa: E731
+    pages, total = model_select(scores, 127, 127, 31, 512, 2, block)
+    assert pages == exact_topk(scores, 127, 127, 31)
+    assert total == 127
+    _, total_rr = model_select(scores, 127, 127, 31, 512, 2, sel_page)
+    assert total_rr <= 64
+    for nt in (256, 512):
+        gs = nt // 64
+        filled = {sel_page(t, 0, nt, False) // gs for t in range(nt)}  # groups with a page < nt
+        assert len(filled) == 64
