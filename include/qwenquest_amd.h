@@ -116,6 +116,31 @@ int qq_quest_prepare_step(const int64_t* seq_lens, int bs, int page_size, int to
                           int avoid_recent_overlap, int32_t* actual_lens,
                           int32_t* candidate_limit, void* stream);
 
+/* Bytes of the sync buffer qq_quest_decode_step takes for `bs` batch entries (one
+ * counter per entry, each on its own 128-byte line). */
+int64_t qq_quest_decode_step_sync_bytes(int bs);
+
+/* Replaces one decode step's Quest bookkeeping as QuestOnlyBackend.init_forward_metadata
+ * runs it, in one launch: the previous token's row per request
+ * (src/qwenquest/attention/quest_only.py:84-97), QuestAlgorithm.update_decode_representations
+ * and maybe_finalize_decode_representations over every layer (src/qwenquest/quest.py:284-321)
+ * and QuestAlgorithm.prepare_step (quest.py:325-362).  The results are those of
+ * qq_quest_decode_step_locs, qq_quest_decode_update (finalize, layers [0, num_layers)) and
+ * qq_quest_prepare_step called in that order, for a batch that lists each request once (as
+ * the reference's batches do; a request listed twice would be folded and advanced once per
+ * entry).  device_locs_out (optional, [bs]) receives the rows looked up.  sync:
+ * qq_quest_decode_step_sync_bytes(bs) bytes, zero before the first call; each call leaves
+ * it zero. */
+int qq_quest_decode_step(const int64_t* req_pool_indices, const int64_t* seq_lens, int bs,
+                         uint8_t* skip_first, const int32_t* req_to_token, int64_t r2t_rows,
+                         int64_t r2t_cols, int64_t r2t_stride, int64_t* device_locs_out,
+                         const void* k_base, int64_t k_layer_stride, int k_dtype, int64_t k_rows,
+                         uint16_t* page_k_bounds, uint16_t* running_k_min, uint16_t* running_k_max,
+                         int32_t* running_token_count, int32_t* running_page_idx, int num_layers,
+                         int max_reqs, int max_pages, int kv_heads, int head_dim, int page_size,
+                         int top_k, int avoid_recent_overlap, int32_t* actual_lens,
+                         int32_t* candidate_limit, void* sync, int64_t sync_bytes, void* stream);
+
 /* Replaces QuestAlgorithm.retrieve_topk (src/qwenquest/quest.py:409-464)
  * including group_queries (:366-391) and page_scores (:393-405), for layer
  * offset `layer`.  q: [bs, num_q_heads, D] (bf16 or fp32) with batch stride

@@ -40,6 +40,12 @@ SIGNATURES: dict[str, tuple] = {
     "qq_quest_decode_finalize": (_I, [_P, _I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P]),
     "qq_quest_prepare_step": (_I, [_P, _I, _I, _I, _I, _P, _P, _P]),
     "qq_quest_decode_step_locs": (_I, [_P, _P, _I, _P, _P, _L, _L, _L, _P, _P]),
+    "qq_quest_decode_step_sync_bytes": (_L, [_I]),
+    "qq_quest_decode_step": (
+        _I,
+        [_P, _P, _I, _P, _P, _L, _L, _L, _P, _P, _L, _I, _L, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I,
+         _P, _P, _P, _L, _P],
+    ),
     "qq_quest_retrieve_topk": (
         _I,
         [_P, _I, _L, _I, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P],

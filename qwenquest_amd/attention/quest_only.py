@@ -69,13 +69,22 @@ class QuestOnlyBackend(AttentionBackend):
         # call (set to None to run the layer as four launches)
         sync_bytes = int(_lib.load().qq_quest_layer_step_sync_bytes(req_to_token_pool.size, token_to_kv_pool.kv_heads))
         self._step_sync = torch.zeros(max(sync_bytes, 4), dtype=torch.uint8, device=device)
+        # counters of the one-launch decode-step bookkeeping, left zeroed by every call
+        step_bytes = int(_lib.load().qq_quest_decode_step_sync_bytes(req_to_token_pool.size))
+        self._decode_sync = torch.zeros(max(step_bytes, 4), dtype=torch.uint8, device=device)
 
     # ---------------------------------------------------------------- per step
 
     def init_forward_metadata(self, batch: ForwardBatch) -> None:
+        """[Q3] + [Q4] for a decode batch in one launch (QuestAlgorithm.decode_step): the
+        same results as _do_quest_decode_step_update followed by prepare_step."""
         if batch.forward_mode.is_decode():
-            self._do_quest_decode_step_update(batch.req_pool_indices, batch.seq_lens)
-            self.quest.prepare_step(batch.seq_lens)
+            bs = int(batch.req_pool_indices.numel())
+            if bs > self._step_locs.numel():
+                raise ValueError(f"batch {bs} exceeds the request pool ({self._step_locs.numel()})")
+            self.quest.decode_step(batch.req_pool_indices, batch.seq_lens, self.token_to_kv_pool.k_all,
+                                   self.req_to_token, self._skip_first_decode_update, self._decode_sync,
+                                   self._step_locs[:bs])
 
     def _do_quest_decode_step_update(self, req_pool_indices: torch.Tensor, seq_lens: torch.Tensor) -> None:
         """[Q3] The previous step's token sits at position ``seq_len - 2`` (quest_only.py:84-97).

@@ -506,6 +506,84 @@ __global__ __launch_bounds__(kThreads) void decode_step_locs_kernel(const int64_
   }
 }
 
+// One decode step's bookkeeping in one launch (quest_only.py:84-97, quest.py:284-321
+// and 325-362): blockIdx.x = batch entry, blockIdx.y = layer.  Every block looks up
+// its entry's previous-token row itself (the lookup of decode_step_locs_kernel), folds
+// that layer (decode_update_kernel with finalize) and counts itself done on the
+// entry's counter; the entry's last block advances the page counters
+// (advance_counters_kernel) and clears the first-step flag, after every block of the
+// entry has read them.  The layer-0 block writes the step layout (prepare_step_kernel).
+struct DecodeStepArgs {
+  const int64_t *rpi, *seq;
+  uint8_t* skip;
+  const int32_t* r2t;
+  int64_t r2t_rows, r2t_cols, r2t_stride;
+  int64_t* locs_out;
+  DecodeArgs d;
+  int n_layers, top_k, avoid;
+  int32_t *actual, *limit;
+  int32_t *count, *page_idx;  // d's counters, advanced by the entry's last block
+  uint32_t* sync;  // one counter per entry, each on its own 128-byte line
+};
+
+__global__ __launch_bounds__(kThreads) void decode_step_kernel(DecodeStepArgs a) {
+  const int i = blockIdx.x;
+  const int li = blockIdx.y;
+  const DecodeArgs& d = a.d;
+  const int64_t r = a.rpi[i];
+  const int64_t s = a.seq[i];
+  if (li == 0 && threadIdx.x == 0) {
+    a.actual[i] = (int32_t)min(s, (int64_t)a.top_k);
+    const int64_t full = s / d.P;
+    a.limit[i] = (int32_t)(a.avoid ? max(full - 1, (int64_t)0) : full);
+  }
+  int64_t row = -1;
+  if (r >= 0 && r < a.r2t_rows && !a.skip[r]) {
+    const int64_t p = max(s - 2, (int64_t)0);
+    if (p < a.r2t_cols) row = a.r2t[r * a.r2t_stride + p];
+  }
+  if (li == 0 && threadIdx.x == 0 && a.locs_out) a.locs_out[i] = row;
+  const bool fold = r >= 0 && r < d.R && row >= 0;
+  if (fold) {
+    const bool row_ok = row < d.k_rows;
+    const bool complete = d.count[r] == d.P - 1;
+    const int64_t page = d.page_idx[r];
+    const void* kl = d.k_base + (int64_t)li * d.k_layer_stride_bytes;
+    for (int c = threadIdx.x; c < d.C; c += kThreads) {
+      const int64_t rc = ((int64_t)li * d.R + r) * d.C + c;
+      uint16_t mn = d.rmin[rc], mx = d.rmax[rc];
+      if (row_ok) {
+        const uint16_t v = load_as_bf16(kl, row * d.C + c, d.k_dtype);
+        mn = bmin(mn, v);
+        mx = bmax(mx, v);
+      }
+      if (complete) {
+        if (page >= 0 && page < d.MP)
+          d.bounds[(((int64_t)li * d.R + r) * d.MP + page) * d.C + c] = pack_pair(mn, mx);
+        d.rmin[rc] = kBf16Max;
+        d.rmax[rc] = kBf16Min;
+      } else {
+        d.rmin[rc] = mn;
+        d.rmax[rc] = mx;
+      }
+    }
+  }
+  // this block's reads of the counters and the flag are done (their values were used)
+  if (threadIdx.x == 0) {
+    uint32_t* cnt = a.sync + (int64_t)i * 32;
+    // agent scope: the entry's blocks run on any of the chip's L2 caches
+    if (__hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)a.n_layers - 1) {
+      __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (fold) {
+        const int32_t c = a.count[r];
+        if (c == d.P - 1) a.page_idx[r] += 1;
+        a.count[r] = (c + 1) % d.P;
+      }
+      if (r >= 0 && r < a.r2t_rows) a.skip[r] = 0;
+    }
+  }
+}
+
 // quest.py:343-352.
 __global__ __launch_bounds__(kThreads) void prepare_step_kernel(const int64_t* seq, int bs, int P, int top_k,
                                                               int avoid, int32_t* actual,
@@ -720,6 +798,70 @@ extern "C" int qq_quest_decode_step_locs(const int64_t* req_pool_indices, const 
   decode_step_locs_kernel<<<1, kThreads, 0, static_cast<hipStream_t>(stream)>>>(
       req_pool_indices, seq_lens, bs, skip_first, req_to_token, r2t_rows, r2t_cols, r2t_stride, device_locs_out);
   return check_launch("qq_quest_decode_step_locs");
+}
+
+extern "C" int64_t qq_quest_decode_step_sync_bytes(int bs) {
+  return bs > 0 ? (int64_t)bs * 32 * (int64_t)sizeof(uint32_t) : 0;
+}
+
+extern "C" int qq_quest_decode_step(const int64_t* req_pool_indices, const int64_t* seq_lens, int bs,
+                                    uint8_t* skip_first, const int32_t* req_to_token, int64_t r2t_rows,
+                                    int64_t r2t_cols, int64_t r2t_stride, int64_t* device_locs_out,
+                                    const void* k_base, int64_t k_layer_stride, int k_dtype, int64_t k_rows,
+                                    uint16_t* page_k_bounds, uint16_t* running_k_min, uint16_t* running_k_max,
+                                    int32_t* running_token_count, int32_t* running_page_idx, int num_layers,
+                                    int max_reqs, int max_pages, int kv_heads, int head_dim, int page_size,
+                                    int top_k, int avoid_recent_overlap, int32_t* actual_lens,
+                                    int32_t* candidate_limit, void* sync, int64_t sync_bytes, void* stream) {
+  const char* what = "qq_quest_decode_step";
+  QQ_REQUIRE(dtype_ok(k_dtype), "%s: unsupported key dtype %d", what, k_dtype);
+  QQ_REQUIRE(bs >= 0 && num_layers > 0 && page_size > 0 && top_k > 0 && r2t_rows >= 0 && r2t_cols >= 0 &&
+                 r2t_stride >= r2t_cols,
+             "%s: bad arguments (batch %d, layers %d, page %d, top_k %d, table %lld x %lld, stride %lld)", what,
+             bs, num_layers, page_size, top_k, (long long)r2t_rows, (long long)r2t_cols, (long long)r2t_stride);
+  if (bs == 0) return QQ_OK;
+  QQ_REQUIRE(req_pool_indices && seq_lens && skip_first && req_to_token && k_base && page_k_bounds &&
+                 running_k_min && running_k_max && running_token_count && running_page_idx && actual_lens &&
+                 candidate_limit,
+             "%s: null pointer", what);
+  QQ_REQUIRE(sync && sync_bytes >= qq_quest_decode_step_sync_bytes(bs), "%s: sync buffer %lld bytes < %lld needed",
+             what, (long long)sync_bytes, (long long)qq_quest_decode_step_sync_bytes(bs));
+  DecodeStepArgs a;
+  a.rpi = req_pool_indices;
+  a.seq = seq_lens;
+  a.skip = skip_first;
+  a.r2t = req_to_token;
+  a.r2t_rows = r2t_rows;
+  a.r2t_cols = r2t_cols;
+  a.r2t_stride = r2t_stride;
+  a.locs_out = device_locs_out;
+  a.d.k_base = static_cast<const char*>(k_base);
+  a.d.k_layer_stride_bytes = k_layer_stride * dtype_size(k_dtype);
+  a.d.k_dtype = k_dtype;
+  a.d.k_rows = k_rows;
+  a.d.reqs = nullptr;
+  a.d.locs = nullptr;
+  a.d.layer_begin = 0;
+  a.d.finalize = 1;
+  a.d.bounds = reinterpret_cast<uint32_t*>(page_k_bounds);
+  a.d.rmin = running_k_min;
+  a.d.rmax = running_k_max;
+  a.d.count = running_token_count;
+  a.d.page_idx = running_page_idx;
+  a.d.R = max_reqs;
+  a.d.MP = max_pages;
+  a.d.C = kv_heads * head_dim;
+  a.d.P = page_size;
+  a.n_layers = num_layers;
+  a.top_k = top_k;
+  a.avoid = avoid_recent_overlap;
+  a.actual = actual_lens;
+  a.limit = candidate_limit;
+  a.count = running_token_count;
+  a.page_idx = running_page_idx;
+  a.sync = static_cast<uint32_t*>(sync);
+  decode_step_kernel<<<dim3(bs, num_layers), kThreads, 0, static_cast<hipStream_t>(stream)>>>(a);
+  return check_launch(what);
 }
 
 extern "C" int qq_quest_prepare_step(const int64_t* seq_lens, int bs, int page_size, int top_k,

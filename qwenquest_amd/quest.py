@@ -313,6 +313,50 @@ class QuestAlgorithm:
         self._step = StepLayout(seq, actual, limit, self.page_size, self.top_k)
         return self._step
 
+    def decode_step(
+        self,
+        req_indices: torch.Tensor,
+        seq_lens: torch.Tensor,
+        k_all: torch.Tensor,
+        req_to_token: torch.Tensor,
+        skip_first: torch.Tensor,
+        sync: torch.Tensor,
+        device_locs_out: torch.Tensor | None = None,
+    ) -> StepLayout:
+        """[Q3] + [Q4] in one launch, as a backend's init_forward_metadata runs them
+        (quest_only.py:84-97, quest.py:284-362): the previous token's row of each request
+        (``req_to_token[req, seq_len - 2]``; none while ``skip_first[req]`` is set, which is
+        then cleared) folded into every layer's running bounds with completed pages
+        finalized, then the step layout.  Equal to the row lookup,
+        update_decode_representations_fused and prepare_step in that order for a batch that
+        lists each request once.  ``sync``: at least qq_quest_decode_step_sync_bytes(bs)
+        zeroed bytes, left zeroed."""
+        self._check_k_all(k_all)
+        rpi = req_indices.to(device=self.device, dtype=torch.int64).contiguous()
+        seq = seq_lens.to(device=self.device, dtype=torch.int64).contiguous()
+        bs = int(seq.numel())
+        if rpi.numel() != bs:
+            raise ValueError("req_indices and seq_lens differ in length")
+        if skip_first.dtype not in (torch.bool, torch.uint8) or not skip_first.is_contiguous():
+            raise ValueError("skip_first must be a contiguous bool or uint8 tensor")
+        if req_to_token.dtype != torch.int32 or req_to_token.dim() != 2 or req_to_token.stride(1) != 1:
+            raise ValueError("req_to_token must be a 2-D int32 tensor with unit column stride")
+        actual = torch.empty(bs, dtype=torch.int32, device=self.device)
+        limit = torch.empty(bs, dtype=torch.int32, device=self.device)
+        k0 = k_all[self.start_layer]
+        _lib.call(
+            "qq_quest_decode_step", _lib.ptr(rpi), _lib.ptr(seq), bs, _lib.ptr(skip_first), _lib.ptr(req_to_token),
+            req_to_token.shape[0], req_to_token.shape[1], req_to_token.stride(0),
+            _lib.ptr(device_locs_out) if device_locs_out is not None else None,
+            _lib.ptr(k0), k_all.stride(0), _lib.dtype_code(k0.dtype), k_all.shape[1],
+            _lib.ptr(self.page_k_bounds), _lib.ptr(self.running_k_min), _lib.ptr(self.running_k_max),
+            _lib.ptr(self.running_token_count), _lib.ptr(self.running_page_idx), *self._geometry(),
+            self.top_k, int(self.avoid_recent_overlap), _lib.ptr(actual), _lib.ptr(limit),
+            _lib.ptr(sync), sync.numel() * sync.element_size(), _lib.stream(self.device),
+        )
+        self._step = StepLayout(seq, actual, limit, self.page_size, self.top_k)
+        return self._step
+
     # ---------------------------------------------------- [Q5] page criticality
 
     def _queries_3d(self, queries: torch.Tensor) -> torch.Tensor:

@@ -834,3 +834,80 @@ def test_decode_step_row_lookup():
               R, view.shape[1], view.stride(0), _lib.ptr(out), _lib.stream(DEV))
     torch.cuda.synchronize()
     assert out[:4].cpu().tolist() == [-1, -1, int(t[2, 5]), int(t[3, 1])]
+
+
+def test_one_launch_decode_step_equals_the_three_stages():
+    """qq_quest_decode_step (QuestAlgorithm.decode_step): the row lookup, the fold of every
+    layer with finalize, and the step layout in one launch equal qq_quest_decode_step_locs,
+    update_decode_representations_fused and prepare_step bit for bit - bounds, running
+    bounds, counters, first-step flags, rows, actual lengths and candidate limits - over 40
+    steps that cross page boundaries, with requests on their first step, a row past the pool
+    and a pool index past the table; the bounds equal the oracle's."""
+    from qwenquest_amd import _lib
+    from qwenquest_amd.memory import MHATokenToKVPool
+
+    L, KV, D, P, R, W = 3, 4, 32, 16, 6, 200
+    rows = R * W
+    kvp = MHATokenToKVPool(rows, L, KV, D, torch.bfloat16, DEV)
+    kvp.k_all.copy_(rand_bf16((L, rows + 1, KV, D), seed=21).to(DEV))
+    host = bf16_bits(kvp.k_all.cpu())
+    perm = torch.randperm(rows, generator=torch.Generator().manual_seed(3)) + 1
+    table = perm.view(R, W).to(torch.int32)
+    table[3, 70] = rows + 500  # a row past the pool: no key folded, counters still advance
+    r2t = table.to(DEV)
+    a, st = new_quest(64, P, L, R, W, KV, D)
+    b, _ = new_quest(64, P, L, R, W, KV, D)
+    prompts = {2: 40, 0: 17, 5: 64, 3: 63}
+    skip_a = torch.zeros(R, dtype=torch.bool, device=DEV)
+    for r, n in prompts.items():
+        idx = r2t[r, :n]
+        a.update_prefill_representations_fused(r, kvp.k_all, idx)
+        b.update_prefill_representations_fused(r, kvp.k_all, idx)
+        for layer in range(L):
+            st.update_prefill_representations(layer, r, host[layer], table[r, :n].numpy())
+        skip_a[r] = r != 3  # request 3 decodes without the first-step skip
+    skip_b = skip_a.clone().to(torch.uint8)
+    skip_a = skip_a.to(torch.uint8)
+    rpi = torch.tensor([2, 0, 5, 3, 9], dtype=torch.int64, device=DEV)  # 9: past the table's rows
+    seq = torch.tensor([prompts[2] + 1, prompts[0] + 1, prompts[5] + 1, prompts[3] + 1, 30], dtype=torch.int64,
+                       device=DEV)
+    sync = torch.zeros(int(_lib.load().qq_quest_decode_step_sync_bytes(5)), dtype=torch.uint8, device=DEV)
+    locs_a = torch.empty(5, dtype=torch.int64, device=DEV)
+    locs_b = torch.empty(5, dtype=torch.int64, device=DEV)
+    skip_host = {r: r != 3 for r in prompts}
+    for step in range(40):
+        lay_a = a.decode_step(rpi, seq, kvp.k_all, r2t, skip_a, sync, locs_a)
+        _lib.call("qq_quest_decode_step_locs", _lib.ptr(rpi), _lib.ptr(seq), 5, _lib.ptr(skip_b), _lib.ptr(r2t),
+                  R, W, W, _lib.ptr(locs_b), _lib.stream(DEV))
+        b.update_decode_representations_fused(rpi, kvp.k_all, locs_b)
+        lay_b = b.prepare_step(seq)
+        torch.cuda.synchronize()
+        assert torch.equal(locs_a, locs_b), step
+        assert torch.equal(skip_a, skip_b), step
+        assert torch.equal(lay_a.actual_lens, lay_b.actual_lens) and torch.equal(
+            lay_a.candidate_limit_i32, lay_b.candidate_limit_i32), step
+        # the oracle folds the same rows
+        want = []
+        for i, r in enumerate(rpi.tolist()):
+            if r >= R or skip_host.get(r, False):
+                want.append(-1)
+            else:
+                want.append(int(table[r, max(int(seq[i]) - 2, 0)]))
+        for r in prompts:
+            skip_host[r] = False
+        assert locs_a.cpu().tolist() == want, step
+        # entries with a row fold it (a row past the pool folds nothing); all of them advance
+        live = [(r, row) for r, row in zip(rpi.tolist(), want) if 0 <= r < R and row >= 0]
+        folded = [(r, row) for r, row in live if row <= rows]
+        if folded:
+            for layer in range(L):
+                st.update_decode_representations(layer, [r for r, _ in folded], host[layer],
+                                                 np.array([row for _, row in folded]))
+        st.maybe_finalize_decode_representations([r for r, _ in live])
+        seq += 1
+    assert sync.count_nonzero().item() == 0
+    for x, y in ((a.page_k_bounds, b.page_k_bounds), (a.running_k_min, b.running_k_min),
+                 (a.running_k_max, b.running_k_max), (a.running_token_count, b.running_token_count),
+                 (a.running_page_idx, b.running_page_idx)):
+        assert torch.equal(x, y)
+    assert_state_equal(a, st)
