@@ -300,7 +300,8 @@ class QuestRun:
         self.rpi = torch.arange(B, device=dev, dtype=torch.int64)
         self.seq_lens = torch.tensor(self.ctxs, device=dev, dtype=torch.int64)
         self.out_loc = torch.empty(B, device=dev, dtype=torch.int64)
-        self.base = torch.from_numpy(table[:, 0].astype(np.int64)).to(dev)
+        # out_cache_loc = the request's first row + seq_len - 1 (one launch per step)
+        self.base_m1 = torch.from_numpy(table[:, 0].astype(np.int64) - 1).to(dev)
         self.r2t_flat = r2t.view(-1)
         self.max_ctx = max_ctx
         self.batch = ForwardBatch(ForwardMode.DECODE, None, None, self.rpi, self.seq_lens, self.out_loc,
@@ -321,7 +322,7 @@ class QuestRun:
 
     def step(self):
         if self.layout == "contiguous":
-            torch.add(self.base, self.seq_lens - 1, out=self.out_loc)
+            torch.add(self.base_m1, self.seq_lens, out=self.out_loc)
         else:  # the new token's row from the table (the engine writes it there, engine.py:232-235)
             self.out_loc.copy_(self.r2t_flat[self.rpi * self.max_ctx + self.seq_lens - 1])
         self.be.init_forward_metadata(self.batch)
@@ -358,7 +359,7 @@ class QuestRun:
         bounds or K/V rows in a cache, as in the step), HIP events on the launch stream."""
         be, batch, L = self.be, self.batch, self.L
         if self.layout == "contiguous":
-            torch.add(self.base, self.seq_lens - 1, out=self.out_loc)
+            torch.add(self.base_m1, self.seq_lens, out=self.out_loc)
         else:
             self.out_loc.copy_(self.r2t_flat[self.rpi * self.max_ctx + self.seq_lens - 1])
         be.quest.prepare_step(self.seq_lens)
