@@ -330,21 +330,15 @@ __device__ inline void finish_block(const StepArgs& a, int bh, int part, float M
   }
 }
 
-// Attention of one (request, KV head, part) by a block of W waves: the block's
-// share of the layout slots, per_wave rows per wave in steps of 16T rows
+// Dense decode's attention of one (request, KV head, part) by a block of W
+// waves: the block's share of the dense layout's slots (positions 0 .. s - 1,
+// attention/dense.py:26-42), per_wave rows per wave in steps of 16T rows
 // (DEPTH steps in flight), the waves combined in LDS.  With one part the
 // block writes the output; else it stores an (m, l, o) partial (agent scope)
 // and the block that completes the (request, KV head) count merges the parts
-// (up to MG at once; GROUPED: more in groups).  ROWS: the pool rows of the
-// slots are given (rows_in, actual) instead of coming from the page list and
-// req_to_token - the same arithmetic over the same slot order.  Otherwise the
-// block first selects its request's pages itself (quest.py:450-452) from the
-// page scores - every block of the request computes the same list - with a
-// KPT x 64W-page selection that aliases the LDS the row table and the wave
-// combine use later.
-template <bool ROWS, int KPT, int W, int T, int DEPTH, int MG, bool GROUPED, int ROWCAP>
-__device__ inline void attend_item(const StepArgs& a, int bh, int part, unsigned char* smem_raw, uint32_t* s_last,
-                                   int32_t* s_pages) {
+// (up to MG at once; GROUPED: more in groups).
+template <int W, int T, int DEPTH, int MG, bool GROUPED, int ROWCAP>
+__device__ inline void attend_item(const StepArgs& a, int bh, int part, unsigned char* smem_raw, uint32_t* s_last) {
   using Smem = HeadSmem<W, ROWCAP>;
   Smem& sm = *reinterpret_cast<Smem*>(smem_raw);
   const SelectArgs& sa = a.s;
@@ -352,58 +346,26 @@ __device__ inline void attend_item(const StepArgs& a, int bh, int part, unsigned
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   const int lo = lane & 15, hi = lane >> 4;
-  const int parts = a.parts;
   const int b = bh / kStepKV, h = bh - b * kStepKV;
-  const int64_t s = ROWS ? 0 : sa.seq[b];
-  const int64_t req = ROWS ? 0 : sa.rpi[b];
-  const int top_k = sa.top_k, P = sa.P, k = sa.k_sel;
-  const bool long_b = !ROWS && needs_selection(sa, s);
-  // actual_lens (quest.py:345)
-  const int n = ROWS ? min(max(a.actual[b], 0), top_k) : (int)min(max(s, (int64_t)0), (int64_t)top_k);
-  const bool r2t_ok = !ROWS && req >= 0 && req < a.r2t_rows;
+  const int64_t s = sa.seq[b];
+  const int64_t req = sa.rpi[b];
+  const int top_k = sa.top_k;  // the table's width: every context fits
+  const int n = (int)min(max(s, (int64_t)0), (int64_t)top_k);
+  const bool r2t_ok = req >= 0 && req < a.r2t_rows;
   // slots [slot_base, slot_base + per_block): per_wave rows per wave, a multiple of
   // the 32-row step; the row table is filled over the whole range (row 0 past n),
   // so every row a step reads is initialised and in range
   const int per_wave = a.per_wave;
   const int per_block = W * per_wave;  // <= ROWCAP
   const int slot_base = part * per_block;
-  if constexpr (KPT > 0) if (long_b && slot_base < k * P) {  // block-uniform: this block attends selected pages
-    SelectSmem<KPT, kThreads>& ss = *reinterpret_cast<SelectSmem<KPT, kThreads>*>(smem_raw);
-    const int lim = (req >= 0 && req < sa.R) ? min(sa.limit[b], sa.MP) : 0;
-    const float* sc = sa.scores + (int64_t)b * sa.MP;
-    float sv[KPT];
-#pragma unroll
-    for (int i = 0; i < KPT; ++i) {
-      const int p = tid + kThreads * i;
-      sv[i] = p < lim ? sc[p] : 0.0f;
-    }
-    select_topk_block<KPT, kThreads>(sv, lim, max(lim, k), k, ss);
-    if (tid < k) s_pages[tid] = ss.order[tid];
-    __syncthreads();  // the list is in s_pages before the row table reuses the LDS
-  }
-  int32_t* pos_out = !ROWS && h == 0 && sa.positions ? sa.positions + (int64_t)b * top_k : nullptr;
-  bool bad_row = false;  // rows mode: a real slot without a row (a failed swap-in) poisons the output
   for (int i0 = 0; i0 < per_block; i0 += kThreads * 4) {
-    int64_t pv[4];
     int64_t rv[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int slot = slot_base + i0 + tid + kThreads * u;
       const bool mine = i0 + tid + kThreads * u < per_block;  // only this block's share is read
-      if (ROWS) {
-        pv[u] = 0;
-        rv[u] = mine && slot < n ? a.rows_in[(int64_t)b * a.rows_stride + slot] : 0;
-        continue;
-      }
-      int64_t p;
-      if (!long_b)
-        p = s <= top_k ? min((int64_t)slot, max(s - 1, (int64_t)0)) : min(max(s - P, (int64_t)0) + slot, s - 1);
-      else if (slot < k * P)
-        p = (int64_t)s_pages[slot / P] * P + slot % P;
-      else
-        p = min(max(s - P, (int64_t)0) + (slot - k * P), s - 1);
-      pv[u] = p;
-      rv[u] = (mine && slot < n && r2t_ok && p >= 0 && p < a.r2t_stride) ? a.r2t[req * a.r2t_stride + p] : 0;
+      const int64_t p = min((int64_t)slot, max(s - 1, (int64_t)0));
+      rv[u] = (mine && slot < n && r2t_ok && p < a.r2t_stride) ? a.r2t[req * a.r2t_stride + p] : 0;
     }
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
@@ -411,9 +373,7 @@ __device__ inline void attend_item(const StepArgs& a, int bh, int part, unsigned
       const int slot = slot_base + i;
       if (i < per_block) {
         const int64_t row = rv[u];
-        if (ROWS && slot < n && row < 0) bad_row = true;
         sm.rows[i] = (slot < n && row >= 0 && row < a.kv_rows) ? (int32_t)row : 0;
-        if (pos_out && slot < top_k) pos_out[slot] = (int32_t)pv[u];
       }
     }
   }
@@ -431,12 +391,7 @@ __device__ inline void attend_item(const StepArgs& a, int bh, int part, unsigned
       }
     }
   }
-  // the row table is in LDS; the position stores and query loads stay in flight
-  bool poison = false;
-  if constexpr (ROWS)
-    poison = __syncthreads_or(bad_row ? 1 : 0) != 0;
-  else
-    lds_barrier();
+  lds_barrier();  // the row table is in LDS; the query loads stay in flight
   // this wave's rows: local [r0, r0 + per_wave), real up to slot n
   constexpr int kStep = 16 * T;
   const int r0 = wave * per_wave;
@@ -462,22 +417,18 @@ __device__ inline void attend_item(const StepArgs& a, int bh, int part, unsigned
       attend_step<T>(ring[j], qb, r_end - (r0 + kStep * i), a.sl2, M, L, o, lo, hi);
     }
   }
-  finish_block<W, MG, GROUPED>(a, bh, part, M, L, o, poison, sm.m, sm.l, sm.o, s_last);
+  finish_block<W, MG, GROUPED>(a, bh, part, M, L, o, false, sm.m, sm.l, sm.o, s_last);
 }
 
 using HeadSmemLaunch = HeadSmem<kHeadWaves, kStepMaxTopK>;
 
-// The attention launch of the fused layer step (and of the dense decode and
-// the attention over given rows): one 8-wave block per (request, KV head,
+// Dense decode's attention launch: one 8-wave block per (request, KV head,
 // part), blockIdx = (request, KV head) * parts + part.
-template <bool ROWS, int KPT>
 __global__ __launch_bounds__(64 * kHeadWaves, 1) void quest_attend_part_kernel(StepArgs a) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   __shared__ uint32_t s_last;
-  __shared__ int32_t s_pages[kMaxSelFused];
   const int bh = blockIdx.x / a.parts, part = blockIdx.x - bh * a.parts;
-  attend_item<ROWS, KPT, kHeadWaves, kHeadTiles, kHeadDepth, kMaxParts, true, kStepMaxTopK>(
-      a, bh, part, smem_raw, &s_last, s_pages);
+  attend_item<kHeadWaves, kHeadTiles, kHeadDepth, kMaxParts, true, kStepMaxTopK>(a, bh, part, smem_raw, &s_last);
 }
 
 // ------------------------------------------------------- per-page-unit attention
@@ -696,15 +647,13 @@ static int device_cu_count() {
   return cached[dev];
 }
 
-// LDS of an attention kernel instance (above the 64 KiB default: opted in once
-// per device).
-template <bool ROWS, int KPT>
+// LDS of the dense attention kernel (above the 64 KiB default: opted in once per
+// device).
 static size_t head_smem_bytes() {
-  static_assert(sizeof(SelectSmem<(KPT > 0 ? KPT : 1), 64 * kHeadWaves>) <= sizeof(HeadSmemLaunch), "aliased LDS");
   static bool opted[64] = {false};
   int dev = 0;
   if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64 && !opted[dev]) {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&quest_attend_part_kernel<ROWS, KPT>),
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&quest_attend_part_kernel),
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)sizeof(HeadSmemLaunch));
     opted[dev] = true;
   }
@@ -795,7 +744,7 @@ extern "C" int qq_quest_fused_step(int q_dtype, int kv_dtype, int new_dtype, int
              : 0;
 }
 
-// The fused attention over given rows (one launch of quest_attend_part_kernel<true>);
+// The fused attention over given rows (one launch of quest_attend_unit_kernel in its rows mode);
 // QQ_OK when launched, 1 when the shape or the buffers do not allow it.
 int qq::attend_rows_fused(const void* q, int64_t q_bstride, int num_q_heads, const void* k_layer, const void* v_layer,
                       int64_t kv_rows, const int64_t* rows, int64_t slots, const int32_t* actual, int bs, float scale,
@@ -908,7 +857,7 @@ extern "C" int qq_dense_forward_decode(const void* q, int q_dtype, int64_t q_bat
   a.G = G;
   a.parts = parts;
   a.per_wave = ceil_div(top_k, parts * kHeadWaves * 32) * 32;
-  quest_attend_part_kernel<false, 0><<<bs * kStepKV * parts, 64 * kHeadWaves, head_smem_bytes<false, 0>(), s>>>(a);
+  quest_attend_part_kernel<<<bs * kStepKV * parts, 64 * kHeadWaves, head_smem_bytes(), s>>>(a);
   return check_launch(what);
 }
 
