@@ -564,11 +564,16 @@ __device__ inline void select_ranked(const float (&sv)[KPT], int lim, int n_eff,
     const uint64_t ci = lane < total ? s.cand[lane] : 0ull;
     const int page = (int)(~(uint32_t)ci);
     my_row0 = (page_rows && lane < total && page >= 0 && page < max_pages) ? page_rows[page] : -1;
+    // every slot below 64 is read (past `total` it holds stale words, whose
+    // comparisons are masked), so that the SHARE reads go out together instead of
+    // one round trip each behind a branch
+    const int wu = __builtin_amdgcn_readfirstlane(w);
     int cnt = 0;
 #pragma unroll
     for (int j = 0; j < SHARE; ++j) {
-      const int jj = w * SHARE + j;
-      cnt += (jj < total && s.cand[jj] > ci) ? 1 : 0;
+      const int jj = wu * SHARE + j;
+      const uint64_t cj = s.cand[jj];
+      cnt += (int)(cj > ci) & (int)(jj < total);
     }
     s.crank[w][lane] = cnt;
     lds_barrier();  // D
