@@ -465,7 +465,11 @@ __global__ __launch_bounds__(64 * W, 8 / W) void quest_attend_unit_kernel(StepAr
   __shared__ uint32_t s_last;
   UnitSmem<KPT, W>& sm = *reinterpret_cast<UnitSmem<KPT, W>*>(smem_raw);
   const SelectArgs& sa = a.s;
-  const int parts = a.parts;
+  int parts = a.parts;
+  // the score buffer and its width are read with the block's coordinates (an empty
+  // asm ties them to `parts`), so that the score loads below go out with the
+  // request's words instead of one round trip after them
+  if constexpr (!ROWS && KPT > 0) __asm__("" : "+s"(parts) : "s"(sa.scores), "s"(sa.MP), "s"(sa.limit));
   const int bh = blockIdx.x / parts, part = blockIdx.x - bh * parts;
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
@@ -475,10 +479,6 @@ __global__ __launch_bounds__(64 * W, 8 / W) void quest_attend_unit_kernel(StepAr
   const int64_t req = ROWS ? 0 : sa.rpi[b];
   const int top_k = sa.top_k, k = sa.k_sel;
   constexpr int P = 64;
-  const bool long_b = !ROWS && needs_selection(sa, s);
-  // actual_lens (quest.py:345)
-  const int n = ROWS ? min(max(a.actual[b], 0), top_k) : (int)min(max(s, (int64_t)0), (int64_t)top_k);
-  const bool r2t_ok = !ROWS && req >= 0 && req < a.r2t_rows;
   const int G = a.G;
   // Q^T as the B operand: query head lo (zero past G), channels 8hi + 32ks
   bf16x8_t qb[4];
@@ -494,17 +494,32 @@ __global__ __launch_bounds__(64 * W, 8 / W) void quest_attend_unit_kernel(StepAr
       }
     }
   }
-  int my_rank = -1, my_page = -1, my_row0 = -1;  // lane s: a survivor's rank, page, first pool row
+  // the scores go out with the request's words (their addresses do not wait for
+  // them): entries past the table re-read its last one and are masked below.  The
+  // scheduling barrier keeps every use of the request's words after these loads, so
+  // that the wait for the words does not come before them, and both branches below
+  // read the scores, so that the loads are not moved into the selecting one
+  float sv[KPT > 0 ? KPT : 1];
+  int lim_raw = 0;
   if constexpr (KPT > 0) {
-    // the scores go out with the request's words (their addresses do not wait for them):
-    // entries past the table re-read its last one and are masked below
     const float* sc = sa.scores + (int64_t)b * sa.MP;
-    float sv[KPT];
 #pragma unroll
     for (int i = 0; i < KPT; ++i) sv[i] = sc[min(tid + NT * i, sa.MP - 1)];
+    lim_raw = sa.limit[b];
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  const bool long_b = !ROWS && needs_selection(sa, s);
+  // actual_lens (quest.py:345)
+  const int n = ROWS ? min(max(a.actual[b], 0), top_k) : (int)min(max(s, (int64_t)0), (int64_t)top_k);
+  const bool r2t_ok = !ROWS && req >= 0 && req < a.r2t_rows;
+  int my_rank = -1, my_page = -1, my_row0 = -1;  // lane s: a survivor's rank, page, first pool row
+  if constexpr (KPT > 0) {
     if (long_b) {  // block-uniform
-      const int lim = (req >= 0 && req < sa.R) ? min(sa.limit[b], sa.MP) : 0;
+      const int lim = (req >= 0 && req < sa.R) ? min(lim_raw, sa.MP) : 0;
       select_ranked<KPT, NT>(sv, lim, max(lim, k), k, sm.sel, nullptr, sa.MP, my_rank, my_page, my_row0);
+    } else {
+#pragma unroll
+      for (int i = 0; i < KPT; ++i) __asm__ volatile("" ::"v"(sv[i]));
     }
   }
   const int units = top_k / P;

@@ -13,9 +13,10 @@ struct SelectArgs {
   const uint32_t* bounds_layer;  // [R, MP, C] (min, max) words of this layer
   const int64_t* rpi;
   const int64_t* seq;
-  const int32_t* limit;
-  int R, MP, KV, D, C, m, P, top_k, k_sel, ppb;
   float* scores;
+  int R, MP;
+  const int32_t* limit;
+  int KV, D, C, m, P, top_k, k_sel, ppb;
   int32_t* positions;
   // optional: store the decoded token's K/V (memory.py:114-120) before attention reads it
   const void* new_k;
