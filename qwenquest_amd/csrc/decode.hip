@@ -216,21 +216,28 @@ __device__ inline void finish_block(const StepArgs& a, int bh, int part, float M
   // each thread one head x 4 channels: the waves' (m, l, o) weighted in wave order
   for (int grp = tid; grp < G * (kMfmaDim / 4); grp += kThreads) {
     const int head = grp >> 5, d4 = (grp & 31) * 4;
+    // every LDS read first (one wait instead of a chain of them), then the sums
+    float mw[W], lw[W];
+    float4 ov[W];
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      mw[w] = sm_m[w][head];
+      lw[w] = sm_l[w][head];
+      ov[w] = *reinterpret_cast<const float4*>(&sm_o[w][head][d4]);
+    }
     float Mx = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < W; ++w) Mx = fmaxf(Mx, sm_m[w][head]);
+    for (int w = 0; w < W; ++w) Mx = fmaxf(Mx, mw[w]);
     float Ls = 0.0f;
     float4 Os = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
     for (int w = 0; w < W; ++w) {
-      const float mw = sm_m[w][head];
-      const float wgt = mw == -INFINITY ? 0.0f : exp2f(mw - Mx);
-      Ls += wgt * sm_l[w][head];
-      const float4 ov = *reinterpret_cast<const float4*>(&sm_o[w][head][d4]);
-      Os.x += wgt * ov.x;
-      Os.y += wgt * ov.y;
-      Os.z += wgt * ov.z;
-      Os.w += wgt * ov.w;
+      const float wgt = mw[w] == -INFINITY ? 0.0f : exp2f(mw[w] - Mx);
+      Ls += wgt * lw[w];
+      Os.x += wgt * ov[w].x;
+      Os.y += wgt * ov[w].y;
+      Os.z += wgt * ov[w].z;
+      Os.w += wgt * ov[w].w;
     }
     if (parts == 1) {
       const bool any = !(Ls <= 0.0f);  // NaN (a poisoned part) stays NaN
