@@ -473,9 +473,9 @@ __global__ __launch_bounds__(64 * W, 8 / W) void quest_attend_unit_kernel(StepAr
   UnitSmem<KPT, W>& sm = *reinterpret_cast<UnitSmem<KPT, W>*>(smem_raw);
   const SelectArgs& sa = a.s;
   int parts = a.parts;
-  // the score buffer and its width are read with the block's coordinates (an empty
-  // asm ties them to `parts`), so that the score loads below go out with the
-  // request's words instead of one round trip after them
+  // the score buffer, its width and the limit array are read with the block's
+  // coordinates (an empty asm ties them to `parts`), so that the score and limit
+  // loads below go out with the request's words instead of one round trip after them
   if constexpr (!ROWS && KPT > 0) __asm__("" : "+s"(parts) : "s"(sa.scores), "s"(sa.MP), "s"(sa.limit));
   const int bh = blockIdx.x / parts, part = blockIdx.x - bh * parts;
   const int tid = threadIdx.x;

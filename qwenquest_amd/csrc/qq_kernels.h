@@ -11,6 +11,8 @@ struct SelectArgs {
   int64_t q_bstride;
   int H;
   const uint32_t* bounds_layer;  // [R, MP, C] (min, max) words of this layer
+  // rpi .. limit adjacent: the attention launch reads them in its first batch of
+  // argument loads
   const int64_t* rpi;
   const int64_t* seq;
   float* scores;
