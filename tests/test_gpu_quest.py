@@ -682,6 +682,83 @@ def test_fused_step_req_to_token_layouts(layout, ctx):
     assert not step_counters(be, len(reqs)).any()
 
 
+
+@pytest.mark.parametrize("case", ["equal_keys", "wide_selection"])
+def test_fused_step_ties_and_wide_selection(case):
+    """The fused step's in-block selection on its slow paths, through QuestOnlyBackend:
+    every key equal (all page scores tie, so every candidate passes the threshold - more
+    than 64 survivors - and the ties break to the lowest page), and top_k 4096 (63 selected
+    pages: the threshold is the 63rd largest of 64 group maxima, so hundreds of pages survive
+    and the ranking counts).  Positions bit-exact vs the oracle over three decode steps,
+    outputs within attn_tol of the oracle's attention over r2t[req, positions]."""
+    from qwenquest_amd.attention.quest_only import QuestOnlyBackend
+    from qwenquest_amd.batch import ForwardBatch, ForwardMode
+    from qwenquest_amd.memory import MHATokenToKVPool, ReqToTokenPool
+
+    H, KV, D, P = 32, 4, 128, 64
+    TOP_K, CTX = (2048, 40000) if case == "equal_keys" else (4096, 20000)
+    prompt = {0: CTX - 100, 1: CTX * 2 // 3, 2: TOP_K + 300}
+    steps, nreq = 3, 3
+    rows_total = nreq * CTX + 1
+    r2t = (1 + np.arange(nreq * CTX)).astype(np.int32).reshape(nreq, CTX)
+    rtp = ReqToTokenPool(nreq, CTX, DEV)
+    rtp.req_to_token.copy_(torch.from_numpy(r2t).to(DEV))
+    kvp = MHATokenToKVPool(rows_total - 1, 1, KV, D, torch.bfloat16, DEV)
+    be = QuestOnlyBackend(rtp, kvp, {"algorithm": "quest", "top_k": TOP_K, "quest_page_size": P})
+    from qwenquest_amd import _lib
+
+    bf = _lib.DTYPE_BF16  # the shape takes the fused (two-launch) layer step
+    assert _lib.load().qq_quest_fused_step(bf, bf, bf, H, KV, D, P, TOP_K, be.quest.max_pages_per_req) == 1
+    st = oq.QuestState(TOP_K, P)
+    st.init_storage(0, 1, nreq, CTX, KV, D)
+    if case == "equal_keys":
+        kk = torch.zeros((1, rows_total, KV, D), dtype=torch.bfloat16)
+    else:
+        kk = rand_bf16((1, rows_total, KV, D), seed=91)
+    vv = rand_bf16((1, rows_total, KV, D), seed=92)
+    kb, vb = bf16.to_f32(bf16_bits(kk)), bf16.to_f32(bf16_bits(vv))
+    kvp.k_all.copy_(kk.to(DEV))
+    kvp.v_all.copy_(vv.to(DEV))
+    for r, n in prompt.items():
+        rows = torch.from_numpy(r2t[r, :n].astype(np.int64))
+        be.quest.update_prefill_representations_fused(r, kvp.k_all, rtp.req_to_token[r, :n])
+        be._skip_first_decode_update[r] = True
+        st.update_prefill_representations(0, r, bf16_bits(kk[0]), rows.numpy())
+    reqs = sorted(prompt)
+
+    class Layer:
+        layer_id, scaling = 0, D**-0.5
+
+    for step in range(steps):
+        seqs = [prompt[r] + step + 1 for r in reqs]
+        locs = torch.tensor([int(r2t[r, s - 1]) for r, s in zip(reqs, seqs)], device=DEV)
+        batch = ForwardBatch(ForwardMode.DECODE, None, None, torch.tensor(reqs, device=DEV),
+                             torch.tensor(seqs, device=DEV), locs, rtp, kvp, be)
+        be.init_forward_metadata(batch)
+        if step > 0:
+            prev = np.array([r2t[r, s - 2] for r, s in zip(reqs, seqs)])
+            st.update_decode_representations(0, reqs, bf16_bits(kk[0]), prev)
+            st.maybe_finalize_decode_representations(reqs)
+        st.prepare_step(seqs)
+        q = rand_bf16((len(reqs), H, D), seed=500 + step)
+        lc = locs.cpu()
+        out = be.forward_decode(q.to(DEV), kk[0, lc].to(DEV), vv[0, lc].to(DEV), Layer(), batch)
+        pos = be._positions[: len(reqs)].clone()
+        ref_pos, ref_actual, _ = st.retrieve_topk(q.float().numpy(), 0, reqs)
+        got_pos = pos.cpu().numpy()
+        rows = []
+        for i, r in enumerate(reqs):
+            n = int(ref_actual[i])
+            assert np.array_equal(got_pos[i, :n], ref_pos[i, :n]), f"{case} step {step} r{r}"
+            rows.append(r2t[r, ref_pos[i, :n]].astype(np.int64))
+        if case == "equal_keys":  # ties: the lowest pages first, then the recent window
+            s0 = seqs[0]
+            want = np.concatenate([np.arange(TOP_K - P), np.arange(s0 - P, s0)])
+            assert np.array_equal(got_pos[0, :TOP_K], want)
+        ref = oa.sparse_decode(q.float().numpy(), kb[0], vb[0], rows, D**-0.5)
+        assert_attn_close(out.float().cpu().numpy(), ref, f"{case} step {step}")
+    assert not step_counters(be, len(reqs)).any()
+
 def test_positions_and_rows_entries_are_bit_identical():
     """qq_quest_decode_attention (positions through req_to_token) and
     qq_decode_attention_rows (rows given) on the same rows give the same bits, with
