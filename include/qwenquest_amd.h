@@ -213,7 +213,7 @@ int qq_decode_attention_rows(const void* q, int q_dtype, int64_t q_batch_stride,
 
 /* 1 when qq_quest_forward_decode with a sync buffer runs the fused layer step
  * for these shapes (bf16, KV*D = 4*128, G <= 16, page 64, at most 64 selected
- * pages, top_k <= 4096, max_pages <= 6144; new_dtype -1 = no new token), else
+ * pages, top_k <= 4096, max_pages <= 8192; new_dtype -1 = no new token), else
  * 0.  No counterpart in the reference: it lets a caller of
  * qq_decode_attention_rows choose the same attention arithmetic. */
 int qq_quest_fused_step(int q_dtype, int kv_dtype, int new_dtype, int num_q_heads, int kv_heads,
@@ -235,7 +235,7 @@ int64_t qq_quest_layer_step_sync_bytes(int bs, int kv_heads);
  * qq_decode_attention_workspace_bytes(bs, top_k, H, D).
  * With `sync` (>= qq_quest_layer_step_sync_bytes, zeroed before the first
  * call) and the shapes of qq_quest_fused_step (bf16 tensors, KV*D = 4*128,
- * page 64, top_k/P - 1 <= 64, max_pages <= 6144), the layer runs as two launches (page
+ * page 64, top_k/P - 1 <= 64, max_pages <= 8192), the layer runs as two launches (page
  * scores + new token, then per (request, KV head, part) the request's selection,
  * layout, attention and the merge of the parts, handed off inside the launch);
  * otherwise, or with sync == NULL, as four launches.  Calls sharing one sync

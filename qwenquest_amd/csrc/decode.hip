@@ -3,7 +3,7 @@
 // token's K/V, select the positions, gather through req_to_token and attend.
 //
 // Fused path (bf16, KV*D = 4*128, page 64, at most 64 selected pages, at most
-// 6144 pages per request, top_k <= 4096, and a zeroed sync buffer from the
+// 8192 pages per request, top_k <= 4096, and a zeroed sync buffer from the
 // caller): two launches.
 //   1. page scores of every long request (score_pages_fast_kernel in select.hip,
 //      one 256-thread block per (request, 32 candidate pages), all resident at
@@ -50,7 +50,8 @@ constexpr int kHeadDepth = 2;        // steps in flight per wave
 constexpr int kMaxParts = 8;         // dense decode: parts merged in one pass
 // The Quest step's attention (quest_attend_unit_kernel): up to kUnitParts blocks
 // per (request, KV head), merged in one pass; the selection of a 4-wave block
-// holds up to 24 scores per thread (6144 pages).
+// holds up to 32 scores per thread (8192 pages; its LDS, 68 KiB, still lets two
+// blocks share a CU).
 constexpr int kUnitParts = 8;
 constexpr int kUnitMinWaves = 4;
 
@@ -706,10 +707,12 @@ static void launch_unit(const StepArgs& a, hipStream_t s) {
   quest_attend_unit_kernel<ROWS, KPT, W><<<blocks, 64 * W, unit_smem_bytes<ROWS, KPT, W>(), s>>>(a);
 }
 
-// The selection's scores per thread for n_max candidate pages (up to 6144).
+// The selection's scores per thread for n_max candidate pages (up to 8192: 32 per
+// thread at W = 4, 16 at W = 8).
 template <int W>
 static void launch_attend_select(const StepArgs& a, int n_max, hipStream_t s) {
   constexpr int kT = 64 * W;
+  constexpr int kMaxKpt = W == 4 ? 32 : 24;
   if (n_max <= 2 * kT) launch_unit<false, 2, W>(a, s);
   else if (n_max <= 4 * kT) launch_unit<false, 4, W>(a, s);
   else if (n_max <= 5 * kT) launch_unit<false, 5, W>(a, s);  // contexts up to 128K + a few pages at W = 8
@@ -718,11 +721,12 @@ static void launch_attend_select(const StepArgs& a, int n_max, hipStream_t s) {
   else if (n_max <= 9 * kT) launch_unit<false, 9, W>(a, s);  // contexts just past 128K at W = 4
   else if (n_max <= 12 * kT) launch_unit<false, 12, W>(a, s);
   else if (n_max <= 16 * kT) launch_unit<false, 16, W>(a, s);
-  else launch_unit<false, 24, W>(a, s);
+  else if (n_max <= 24 * kT) launch_unit<false, 24, W>(a, s);
+  else launch_unit<false, kMaxKpt, W>(a, s);  // contexts past 384K tokens at W = 4
 }
 
 // Shapes the fused layer step takes (bf16, KV*D = 4*128, G <= 16, page 64, at
-// most 64 selected pages, top_k <= 4096, at most 6144 pages per request).
+// most 64 selected pages, top_k <= 4096, at most 8192 pages per request).
 // new_dtype < 0: no new token.
 static bool fused_shape(int q_dtype, int kv_dtype, int new_dtype, int num_q_heads, int kv_heads, int head_dim,
                         int page_size, int top_k, int max_pages) {
@@ -731,7 +735,7 @@ static bool fused_shape(int q_dtype, int kv_dtype, int new_dtype, int num_q_head
     return false;
   return q_dtype == QQ_DTYPE_BF16 && kv_dtype == QQ_DTYPE_BF16 && (new_dtype < 0 || new_dtype == QQ_DTYPE_BF16) &&
          num_q_heads / kv_heads <= kStepMaxG && top_k / page_size - 1 <= kMaxSelFused && top_k <= kStepMaxTopK &&
-         max_pages <= 24 * 64 * kUnitMinWaves;
+         max_pages <= 32 * 64 * kUnitMinWaves;
 }
 
 // Launch shape of the unit attention: W waves per block, `parts` blocks per (request,

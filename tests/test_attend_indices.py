@@ -32,6 +32,7 @@ PARTS_MAX = 8
 HEAD_WAVES, HEAD_TILES, HEAD_ROWCAP = 8, 2, 4096
 MAX_SEL, MAX_TOPK, MAX_G, KV, UNIT = 64, 4096, 16, 4, 64
 KPT_FORMS = (2, 4, 5, 6, 8, 9, 12, 16, 24)
+KPT_MAX = {4: 32, 8: 24}  # the last form of each block width
 CUS = 256
 
 
@@ -60,7 +61,7 @@ def kpt_form(max_pages, k_sel, nt):
     for kpt in KPT_FORMS:
         if n_max <= kpt * nt:
             return kpt
-    return 24
+    return KPT_MAX[nt // 64]
 
 
 def rank_select_smem_bytes(kpt, nt):
@@ -175,7 +176,7 @@ def check_selection(top_k, page, max_pages, lim, waves):
     # survivors are a subset of the block's nt*kpt keys: cand holds nt*kpt + 64
     assert nt * kpt <= nt * kpt + 64
     smem = unit_smem_bytes(kpt, waves)
-    assert smem <= (64 * 1024 if waves == 4 else 160 * 1024)
+    assert smem <= (80 * 1024 if waves == 4 else 160 * 1024)  # two 4-wave blocks share a CU's 160 KiB
 
 
 TOPKS = (64, 128, 192, 256, 1024, 2048, 2112, 4032, 4096)
@@ -216,11 +217,13 @@ def test_rows_mode_actual_lengths(top_k):
         check_units(top_k, min(max(actual, 0), top_k), 16)
 
 
-@pytest.mark.parametrize("max_pages", (2, 64, 512, 513, 1024, 2049, 2050, 2304, 2305, 2560, 2561, 3072, 4096, 6144))
+@pytest.mark.parametrize("max_pages", (2, 64, 512, 513, 1024, 2049, 2050, 2304, 2305, 2560, 2561, 3072, 4096, 6144,
+                                       6145, 7040, 8192))
 @pytest.mark.parametrize("waves", (4, 8))
 def test_selection_forms(max_pages, waves):
     """The KPT form the host picks holds every candidate page: 2304 / 2560 (contexts just
-    past 128K at 4 / 8 waves), 3072, 6144 pages and the forms between."""
+    past 128K at 4 / 8 waves), 3072, 6144, 8192 pages (the fused step's limit) and the
+    forms between."""
     for top_k, page in ((64, 64), (128, 64), (2048, 64), (4096, 64), (4160, 64)):
         if top_k // page - 1 > MAX_SEL:
             continue

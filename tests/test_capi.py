@@ -110,8 +110,8 @@ def test_fused_step_predicate_without_gpu(lib):
     bf, f32 = _lib.DTYPE_BF16, _lib.DTYPE_F32
     # the benchmark shape: 32 q / 4 KV heads x 128, page 64, top_k 2048, 2049 pages
     assert lib.qq_quest_fused_step(bf, bf, bf, 32, 4, 128, 64, 2048, 2049) == 1
-    assert lib.qq_quest_fused_step(bf, bf, -1, 32, 4, 128, 64, 2048, 6144) == 1  # no new token; 6144 pages
-    assert lib.qq_quest_fused_step(bf, bf, bf, 32, 4, 128, 64, 2048, 6145) == 0  # too many pages
+    assert lib.qq_quest_fused_step(bf, bf, -1, 32, 4, 128, 64, 2048, 8192) == 1  # no new token; 8192 pages
+    assert lib.qq_quest_fused_step(bf, bf, bf, 32, 4, 128, 64, 2048, 8193) == 0  # too many pages
     assert lib.qq_quest_fused_step(bf, bf, bf, 32, 4, 128, 16, 2048, 2049) == 0  # page 16
     assert lib.qq_quest_fused_step(bf, bf, bf, 32, 4, 128, 64, 4224, 2049) == 0  # 65 selected pages
     assert lib.qq_quest_fused_step(bf, bf, f32, 32, 4, 128, 64, 2048, 2049) == 0  # fp32 new token

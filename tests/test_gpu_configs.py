@@ -337,18 +337,21 @@ def test_batch4_262k_outliers_quest_and_hisparse(avoid):
                 assert_attn_close(outs[step, i].float().numpy(), ref, f"step {step} request {i}")
 
 
-def test_contexts_past_the_fused_selection_400k():
-    """Batch 2 x 400000 tokens (6250 pages, past the 6144 pages the fused step selects from,
-    so QuestOnlyBackend runs the four-launch path), 80 decode steps that complete page 6250:
-    QuestOnlyBackend and QuestHiSparseBackend give bit-identical positions and outputs at
-    every step; positions bit-exact vs the oracle on sampled steps, attention within attn_tol."""
+@pytest.mark.parametrize("S,fused", [(450000, True), (540000, False)])
+def test_contexts_past_384k(S, fused):
+    """Batch 2 x 450000 tokens (7032 pages: the fused step's widest selection form, 32
+    scores per thread) and 2 x 540000 (8438 pages, past the 8192 the fused step selects
+    from, so QuestOnlyBackend runs the four-launch path), 80 decode steps that complete a
+    page: QuestOnlyBackend and QuestHiSparseBackend give bit-identical positions and outputs
+    at every step; positions bit-exact vs the oracle on sampled steps, attention within
+    attn_tol."""
     from qwenquest_amd import _lib
     from qwenquest_amd.batch import ForwardBatch, ForwardMode
 
-    B, S, steps = 2, 400000, 80
+    B, steps = 2, 80
     ctx = S + steps + 64
-    assert not _lib.load().qq_quest_fused_step(_lib.DTYPE_BF16, _lib.DTYPE_BF16, _lib.DTYPE_BF16, H, KV, D, P, TOP_K,
-                                               (ctx + P - 1) // P)
+    assert _lib.load().qq_quest_fused_step(_lib.DTYPE_BF16, _lib.DTYPE_BF16, _lib.DTYPE_BF16, H, KV, D, P, TOP_K,
+                                           (ctx + P - 1) // P) == int(fused)
     k = dev_randn((B * ctx + 1, KV, D), 31).to(torch.bfloat16)
     v = dev_randn((B * ctx + 1, KV, D), 32).to(torch.bfloat16)
     qs = dev_randn((steps, B, H, D), 33).to(torch.bfloat16)
